@@ -1,0 +1,253 @@
+#!/usr/bin/env python3
+"""Flash-DMLA benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--secondary prefill,decode] [--no-cpu-baseline]
+
+Primary line (BASELINE.json metric, config 2): cache-latent DMLA prefill forward, bf16, causal,
+B=4, H=16, S=2048, Q [B,H,S,576], shared K_lat [B,S,576], V_lat = K_lat[..., :512], scale
+1/sqrt(192), inputs N(0,1)*0.5 (synthetic, seeded).  One step = one forward launch over the
+whole batch with inputs resident in HBM.  value = algorithmic TFLOP/s over the K timed steps,
+counting B*H*S(S+1)*(576+512) flops (unmasked causal pairs only).
+
+`roofline` times the kernel itself with HIP events recorded on the stream it is launched on;
+`traffic` comes from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary when present.
+`cpu_baseline` times the fp32 PyTorch eager oracle (oracle/dmla_ref.py) on the host cores on
+a bounded sample of the same workload.  `secondary` carries the paged decode (config 3) in
+KV GB/s with its own HBM roofline, timed the same way with rotating KV pools larger than the
+256 MB MALL.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "ds-flashdmla-moe_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 flop/clk/CU)
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+SCALE = 1.0 / math.sqrt(192.0)
+
+
+def _seeded(shape, seed, scale, dtype):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def _load_traffic(name):
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def _time_launches(fn, steps, warmup):
+    """Runs fn() warmup times, then `steps` timed times.  Returns (wall ms/step, kernel ms/launch).
+
+    Wall time is bracketed by torch.cuda.synchronize() on both sides; per-launch durations
+    come from HIP events recorded on the current stream, which is the stream the C ABI
+    receives and launches on.
+    """
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        fn(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    kern_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
+    return wall_ms, kern_ms
+
+
+def bench_prefill(steps, warmup, cpu_baseline):
+    import torch
+
+    from python import ops
+
+    B, H, S = 4, 16, 2048
+    dev = torch.device("cuda:0")
+    q = _seeded((B, H, S, 576), 0, 0.5, torch.bfloat16).to(dev)
+    k = _seeded((B, S, 576), 1, 0.5, torch.bfloat16).to(dev)
+    flops = B * H * S * (S + 1) * (576 + 512)
+
+    def step(i=0):
+        ops.flash_dmla_fwd(q, k, 512, SCALE, True)
+
+    wall_ms, kern_ms = _time_launches(step, steps, warmup)
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    res = {
+        "metric": "DMLA prefill TFLOP/s (cache-latent fwd, config 2)",
+        "value": flops / (wall_ms * 1e-3) / 1e12,
+        "unit": "TFLOP/s",
+        "ms_per_step": wall_ms,
+        "config": {"workload": "cache-latent prefill fwd (BASELINE config 2)", "batch": B, "heads": H,
+                   "seq_len": S, "d_qk": 576, "d_v": 512, "causal": True, "softmax_scale": SCALE},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": _load_traffic("prefill"),
+                     "kernel": "mqa_fwd_kernel<false>", "kernel_ms": kern_ms,
+                     "algorithmic_flops_per_launch": flops},
+    }
+    if cpu_baseline:
+        res["cpu_baseline"] = cpu_prefill(q.cpu(), k.cpu())
+    return res
+
+
+def cpu_prefill(q, k):
+    """fp32 eager oracle on a bounded sample: batch element 0 (all 16 heads, S=2048)."""
+    import torch
+
+    from oracle import dmla_ref as R
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    qs, ks = q[:1].float(), k[:1].float()
+    S, H = qs.shape[2], qs.shape[1]
+    flops = H * S * (S + 1) * (576 + 512)
+    R.dmla_fwd_cache_latent(qs[:, :, :256], ks[:, :256], 512, SCALE, True)  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        R.dmla_fwd_cache_latent(qs, ks, 512, SCALE, True)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": "config 2 batch element 0 (16 heads x 2048 causal), fp32 eager oracle, median of 3",
+            "seconds": t}
+
+
+def bench_decode(steps, warmup, cpu_baseline):
+    import torch
+
+    from python import ops
+
+    B, H, P = 64, 128, 64
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(3)
+    lens = torch.randint(1024, 8193, (B,), generator=g)
+    n_pages = (lens + P - 1) // P
+    total = int(n_pages.sum())
+    max_pages = int(n_pages.max())
+    # Three rotating pools (each ~340 MB) so every step streams KV that is not in the 256 MB MALL.
+    pools, tables = [], []
+    for r in range(3):
+        gr = torch.Generator().manual_seed(100 + r)
+        pools.append((torch.randn(total, P, 576, generator=gr) * 0.5).to(torch.bfloat16).to(dev))
+        perm = torch.randperm(total, generator=gr)
+        table = torch.zeros(B, max_pages, dtype=torch.int32)
+        c = 0
+        for b in range(B):
+            n = int(n_pages[b])
+            table[b, :n] = perm[c:c + n].to(torch.int32)
+            c += n
+        tables.append(table.to(dev))
+    q = _seeded((B, H, 576), 4, 0.5, torch.bfloat16).to(dev)
+    sl = lens.to(torch.int32).to(dev)
+    kv_bytes = int(lens.sum()) * 576 * 2
+    bytes_total = kv_bytes + q.numel() * 2 + B * H * 512 * 2 + tables[0].numel() * 4 + B * 4
+
+    def step(i=0):
+        r = i % 3
+        ops.flash_dmla_decode_paged(q, pools[r], tables[r], sl, 512, SCALE)
+
+    wall_ms, kern_ms = _time_launches(step, steps, warmup)
+    achieved = bytes_total / (kern_ms * 1e-3) / 1e9
+    res = {
+        "metric": "DMLA paged decode KV GB/s (config 3)",
+        "value": bytes_total / (wall_ms * 1e-3) / 1e9,
+        "unit": "GB/s",
+        "ms_per_step": wall_ms,
+        "config": {"workload": "paged decode (BASELINE config 3)", "batch": B, "heads": H, "page": P,
+                   "ctx_sum": int(lens.sum()), "ctx_min": int(lens.min()), "ctx_max": int(lens.max())},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": _load_traffic("decode"),
+                     "kernel": "mqa_fwd_kernel<true> + decode_combine_kernel", "kernel_ms": kern_ms,
+                     "algorithmic_bytes_per_launch": bytes_total},
+    }
+    if cpu_baseline:
+        res["cpu_baseline"] = cpu_decode(q.cpu(), pools[0].cpu(), tables[0].cpu(), lens.to(torch.int32), bytes_total)
+    return res
+
+
+def cpu_decode(q, pool, table, lens, bytes_total):
+    """fp32 eager oracle (gather through the block table + attention) on 8 of the 64 sequences."""
+    import torch
+
+    from oracle import dmla_ref as R
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    n = 8
+    sample_bytes = bytes_total * float(lens[:n].sum()) / float(lens.sum())
+    R.dmla_decode_paged(q[:1].float(), pool, table[:1], lens[:1], 512, SCALE)  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        R.dmla_decode_paged(q[:n].float(), pool, table[:n], lens[:n], 512, SCALE)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    return {"value": sample_bytes / t / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"config 3 sequences 0..{n - 1} (ctx sum {int(lens[:n].sum())}), fp32 eager oracle, median of 3",
+            "seconds": t}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--secondary", default="decode", help="comma list of extra workloads: decode")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs and reports the "
+              "single-GPU path, see DESIGN.md for how it would shard", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    cpu = not args.no_cpu_baseline
+    primary = bench_prefill(args.steps, args.warmup, cpu)
+    secondary = {}
+    for name in [s for s in args.secondary.split(",") if s]:
+        if name == "decode":
+            secondary["decode"] = bench_decode(args.steps, args.warmup, cpu)
+        else:
+            raise SystemExit(f"unknown secondary workload {name}")
+    line = {
+        "metric": primary["metric"],
+        "value": primary["value"],
+        "unit": primary["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": primary["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)*0.5 inputs of the BASELINE config 2 shapes)",
+        "config": primary["config"],
+        "roofline": primary["roofline"],
+        "cpu_baseline": primary.get("cpu_baseline"),
+        "secondary": secondary,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,85 @@
+// Device-side building blocks shared by every Flash-DMLA kernel (gfx950 / CDNA4 only).
+//
+// Lane layouts below were checked on MI355X with an in-bounds probe of each builtin:
+//  * v_mfma_f32_16x16x32_bf16: A[16x32] lane l holds A[l%16][8*(l/16)+j], j=0..7;
+//    B[32x16] lane l holds B[8*(l/16)+j][l%16]; C[16x16] lane l holds C[4*(l/16)+i][l%16].
+//  * global_load_lds (16 B): lane l writes its 16 bytes at lds_base + 16*l.
+//  * ds_read_b64_tr_b16: inside each group of 16 lanes, output lane j element e is element
+//    (j%4) of the 8 bytes addressed by lane 4*e + j/4.  Reading row-major [k][n] data with
+//    lane 4e+q addressing row k0+e, columns n0+4q..n0+4q+3 therefore hands lane j the
+//    column n0+j for rows k0..k0+3 -- an MFMA operand with k running along the rows.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dmla {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define DMLA_LDS __attribute__((address_space(3)))
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+
+__device__ __forceinline__ f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+// Wave-uniform value of an expression that is already uniform (moves it to an SGPR).
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// 16-byte direct global->LDS copy of one wave: lane l reads sbase + voff (voff per lane) and
+// lands at LDS byte address lds_addr + 16*l.  Issued as inline assembly so the compiler does not
+// treat the in-flight copy as aliasing every later LDS read (it would wait for the copy before
+// the first one); completion is awaited explicitly with s_waitcnt vmcnt before the barrier that
+// publishes the tile.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved: the clobber only documents it
+__device__ __forceinline__ void dma16(const void* sbase, unsigned voff, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(sbase)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ unsigned lds_addr(const DMLA_LDS void* p) {
+  return (unsigned)(uintptr_t)p;
+}
+
+__device__ __forceinline__ bf16x4 lds_read_tr16(const DMLA_LDS bf16x4* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(const_cast<DMLA_LDS bf16x4*>(p));
+}
+
+__device__ __forceinline__ bf16x8 lds_read_b128(const DMLA_LDS bf16x8* p) { return *p; }
+
+__device__ __forceinline__ bf16x8 concat(const bf16x4& a, const bf16x4& b) {
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Cross-lane butterflies among the four 16-lane groups of a wave (the groups that share one
+// MFMA column): lanes l, l^16, l^32, l^48.
+__device__ __forceinline__ float xor_lanes(float v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+__device__ __forceinline__ float group_max(float v) {
+  v = fmaxf(v, xor_lanes(v, 16));
+  return fmaxf(v, xor_lanes(v, 32));
+}
+__device__ __forceinline__ float group_sum(float v) {
+  v += xor_lanes(v, 16);
+  return v + xor_lanes(v, 32);
+}
+
+// Wait until every outstanding vector-memory op of this wave (including LDS DMA) has landed.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); /* gfx9 encoding: vmcnt(0) expcnt(7) lgkmcnt(15) */ }
+
+}  // namespace dmla

@@ -1,0 +1,637 @@
+// Flash-DMLA forward over a shared 576-wide latent cache: cache-latent prefill and paged decode.
+//
+// Semantics follow the reference's online-softmax forward (csrc/attention/fa2_fwd.cu:9-133 for
+// the tile loop, csrc/attention/fa_fwd.cu:81-123 for the m/l/alpha recurrence and the 1/l guard)
+// applied to the DMLA cache-latent mode of README.md:15: every head of a batch attends the same
+// latent rows K_lat[b] (d_qk = 576 = 512 latent + 64 rope) and V_lat = K_lat[..., :512].
+//
+// MI355X design (one kernel family for both paths):
+//  * A workgroup owns 64 query rows.  Rows are (position, head) pairs with the head fastest, so
+//    all heads of a position share one causal limit and the workgroup streams ONE latent key
+//    sequence: prefill is multi-query attention with M = 64 rows per key tile, decode puts 64
+//    heads of one sequence in M.
+//  * 4 waves, one per SIMD, arranged as 2 pairs.  A pair owns 32 rows; its two waves split the
+//    work in halves: wave half h holds Q[:, 288h .. 288h+287] (72 VGPRs) and accumulates
+//    O[:, 256h .. 256h+255] (128 fp32 AGPR/VGPRs).  Partial scores over each half of the 576
+//    dims are summed through LDS.  Every byte of K/V read from LDS feeds 32 rows, as in a
+//    32-rows-per-wave design, at ~300 instead of ~470 live registers per lane.
+//  * Key tiles of 32 rows x 576 (36 KB) are copied global -> LDS with 16-byte direct loads
+//    (no VGPR staging) into a 3-deep ring, two tiles ahead of use.
+//  * S^T = K_tile . Q^T on v_mfma_f32_16x16x32_bf16 leaves each lane holding one query's scores
+//    for keys {4g..4g+3, 16+4g..16+4g+3}: exactly the B-operand layout PV needs.  PV
+//    (O^T += V^T P^T) reads V^T with ds_read_b64_tr_b16 from the same row-major tile.
+//  * Softmax in the exp2 domain against a reference max fixed at the first finite tile: p stays
+//    below 2^kHeadroom, so O is never rescaled inside the loop.  Scores climbing past that
+//    headroom trigger a recomputation of the row tile against its exact row max.
+#include "dmla_common.h"
+#include "dmla_host.h"
+
+namespace dmla {
+namespace {
+
+constexpr int kDqk = 576;
+constexpr int kDv = 512;
+constexpr int kPage = 64;                           // decode page size (tokens)
+constexpr int kTileN = 32;                          // keys per LDS tile
+constexpr int kGroups = kDqk / 64;                  // 9 chunk groups of 64 columns (128 B)
+constexpr int kGroupBytes = kTileN * 128;           // 4 KB: one chunk group of all tile rows
+constexpr int kTileBytes = kGroups * kGroupBytes;   // 36 KB
+constexpr int kRing = 3;                            // tiles in flight
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRowsPerWG = 64;
+constexpr int kKcHalf = kDqk / 32 / 2;              // 9 k-steps per dims half
+constexpr int kDbHalf = kDv / 16 / 2;               // 16 output column blocks per half
+constexpr int kDmaPerWave = kTileBytes / 1024 / kWaves;  // 9 one-KB DMA instructions
+constexpr int kXBytes = kWaves * 4096;              // partial-score exchange, one buffer
+constexpr int kMaxSplitPages = 1024;                // page-table cache of one decode split
+constexpr int kLdsBytes = kRing * kTileBytes + 2 * kXBytes + kMaxSplitPages * 4;
+constexpr float kHeadroom = 32.0f;                  // log2 headroom of p over the reference max
+constexpr int kPrefetch = 4;                        // operand loads kept ahead of the MFMAs
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+static_assert(kPage % kTileN == 0, "a page holds whole tiles");
+
+// LDS tile layout: [chunk group cg (9)][row (32)][8 sixteen-byte chunks], 128 B per row slice,
+// so rows 2k and 2k+1 fall in opposite halves of the 64 x 4-byte banks.  The chunk at logical
+// position j of row r sits at physical position j ^ swz(r & 15), where swz maps the 8 rows of
+// either bank half bijectively onto 0..7 and keeps the pair index (bits 1-2) distinct across
+// 4 consecutive same-half rows.  Both operand reads are then conflict-free: 16 lanes reading
+// one 16-byte chunk of rows r..r+15 (b128 K operand) and 32 lanes reading 32-byte column pairs
+// of rows r..r+7 (ds_read_b64_tr_b16 V operand).
+__host__ __device__ constexpr int swz(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
+
+// Scheduling template for an unrolled region of `steps` steps, each made of `reads` LDS reads
+// feeding 2 MFMAs: `prefetch` steps of reads first, then (2 MFMA, reads) pairs, then the
+// remaining MFMAs.  Keeps the scheduler from hoisting every read (and its registers) to the top.
+template <int steps, int reads, int prefetch>
+__device__ __forceinline__ void pipeline_schedule() {
+  __builtin_amdgcn_sched_group_barrier(0x100, reads * prefetch, 0);
+#pragma unroll
+  for (int i = 0; i < steps - prefetch; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, reads, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < prefetch; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+}
+
+struct MqaParams {
+  const bf16* q;
+  const bf16* kv;
+  bf16* o;
+  float* m;        // prefill statistics (nullable)
+  float* l;
+  float* lse;      // decode log-sum-exp (nullable)
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_ss;  // prefill: batch/row strides of K_lat; decode: page/row strides
+  int64_t o_sb, o_sh, o_ss;
+  int B, H, Sq, Sk;
+  float scale_log2;    // softmax_scale * log2(e)
+  int causal;
+  int n_row_tiles;     // prefill: ceil(H*Sq / 64)
+  // decode
+  const int32_t* block_table;
+  const int32_t* seqlens;
+  int64_t bt_sb;
+  int num_pages;
+  int max_pages;
+  int pages_per_split;
+  int max_splits;
+  int head_groups;     // ceil(H / 64)
+  int n_units;         // B * max_splits
+  float* part_o;       // [B, max_splits, H, 512] normalised partial outputs
+  float* part_lse;     // [B, max_splits, H]
+};
+
+struct Work {
+  int b, row0, tile_begin, tile_end, split, nsplit, ctx, page_begin;
+};
+
+template <bool kDecode, int kHalf>
+__device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const Work& wk, DMLA_LDS char* lds,
+                                             const int wave, const int lane) {
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
+  const int pair = wave >> 1;
+  const int b = wk.b, row0 = wk.row0, tile_begin = wk.tile_begin, tile_end = wk.tile_end;
+  DMLA_LDS char* xbuf = lds + kRing * kTileBytes;
+  const DMLA_LDS int* page_cache = reinterpret_cast<const DMLA_LDS int*>(xbuf + 2 * kXBytes);
+
+  const int nrows = kDecode ? p.H : p.H * p.Sq;
+  auto row_of = [&](int qg) { return row0 + pair * 32 + qg * 16 + l16; };
+  auto limit_of = [&](int r) -> int {
+    if constexpr (!kDecode) {
+      const int pos = r / p.H;
+      return p.causal ? min(pos + (p.Sk - p.Sq), p.Sk - 1) : p.Sk - 1;
+    } else {
+      return wk.ctx - 1;
+    }
+  };
+  // Tiles whose last key is <= the smallest limit in the workgroup need no mask.
+  const int wg_min_lim = limit_of(row0);
+
+  // ---- Q half as MFMA B operand: lane holds Q[row 16qg+l16][288 half + 32c + 8g .. +7] ----
+  bf16x8 qreg[2][kKcHalf];
+#pragma unroll
+  for (int qg = 0; qg < 2; ++qg) {
+    const int r = row_of(qg) < nrows ? row_of(qg) : 0;
+    const bf16* qrow;
+    if constexpr (!kDecode) {
+      const int pos = r / p.H, head = r - pos * p.H;
+      qrow = p.q + b * p.q_sb + head * p.q_sh + pos * p.q_ss;
+    } else {
+      qrow = p.q + b * p.q_sb + r * p.q_sh;
+    }
+    qrow += kHalf * (kDqk / 2) + 8 * g;
+#pragma unroll
+    for (int c = 0; c < kKcHalf; ++c) qreg[qg][c] = *reinterpret_cast<const bf16x8*>(qrow + 32 * c);
+  }
+  // Q must have landed before the first tile copy is issued: the compiler does not count the
+  // (inline assembly) copies, so a later wait of its own for Q would drain them too.
+  wait_vmem();
+
+  // ---- tile staging ----------------------------------------------------------------------
+  // DMA instruction i (0..35) fills LDS bytes [1024 i, 1024 i + 1024) of the slot = chunk group
+  // i/4, rows 8(i%4) .. +7.  Lane l covers row 8(i%4) + l/8 at physical chunk l%8, i.e.
+  // logical chunk (l%8) ^ swz(row & 15), which depends only on the lane and on bit 3 of row.
+  bool bad_page = false;
+  const int row_stride_bytes = (int)(p.k_ss * 2);
+  const int dma_lane_row = lane >> 3;
+  const unsigned dma_off0 = dma_lane_row * row_stride_bytes + 16 * ((lane & 7) ^ swz(dma_lane_row));
+  const unsigned dma_off8 = dma_lane_row * row_stride_bytes + 16 * ((lane & 7) ^ swz(dma_lane_row + 8));
+  const unsigned dma_row0_off = 16 * ((lane & 7) ^ swz(0));
+  const unsigned lds_base = lds_addr(lds);
+  auto stage = [&](int tile) {
+    const char* tile_base;
+    int valid_rows;
+    if constexpr (!kDecode) {
+      tile_base = reinterpret_cast<const char*>(p.kv + b * p.k_sb + (int64_t)tile * kTileN * p.k_ss);
+      valid_rows = p.Sk - tile * kTileN;
+    } else {
+      const int pg = tile / (kPage / kTileN);
+      int page = uniform(page_cache[pg - wk.page_begin]);
+      if (page < 0 || page >= p.num_pages) { bad_page = true; page = 0; }
+      tile_base = reinterpret_cast<const char*>(p.kv + (int64_t)page * p.k_sb +
+                                                (int64_t)(tile % (kPage / kTileN)) * kTileN * p.k_ss);
+      valid_rows = wk.ctx - tile * kTileN;
+    }
+    const unsigned dst = lds_base + ((tile - tile_begin) % kRing) * kTileBytes;
+    if (valid_rows >= kTileN) {
+#pragma unroll
+      for (int j = 0; j < kDmaPerWave; ++j) {
+        const int i = j * kWaves + wave;
+        const int r0 = 8 * (i & 3), cg = i >> 2;
+        dma16(tile_base + (r0 * row_stride_bytes + cg * 128), (r0 & 8) ? dma_off8 : dma_off0, dst + i * 1024);
+      }
+    } else {
+      // Rows past the valid range re-read row 0 of the tile: finite data, masked later.
+#pragma unroll
+      for (int j = 0; j < kDmaPerWave; ++j) {
+        const int i = j * kWaves + wave;
+        const int r0 = 8 * (i & 3), cg = i >> 2;
+        const bool ok = r0 + dma_lane_row < valid_rows;
+        const unsigned off = ok ? (unsigned)(r0 * row_stride_bytes) + ((r0 & 8) ? dma_off8 : dma_off0) : dma_row0_off;
+        dma16(tile_base + cg * 128, off, dst + i * 1024);
+      }
+    }
+  };
+  // Wait for this wave's DMA of the tile about to be used; the next tile's may stay in flight.
+  auto wait_tile = [&](int t) {
+    if (t + 1 < tile_end) __builtin_amdgcn_s_waitcnt(0x0f70 | kDmaPerWave);  // vmcnt(9)
+    else wait_vmem();
+  };
+
+  // ---- per-lane LDS byte offsets -----------------------------------------------------------
+  // K operand (A of S^T) for global k-step c: row 16kb + l16, logical chunk 4c + g = chunk
+  // group c/2, in-group position 4(c&1) + g.
+  const int ksw = swz(l16);
+  const int k_off[2] = {l16 * 128 + 16 * (g ^ ksw), l16 * 128 + 16 * ((4 + g) ^ ksw)};
+  // V operand (A of O^T) through transpose reads: lane 4e+q of group g reads row 4g+e (and
+  // 16+4g+e), columns 16db + 4q .. +3 = chunk group db/4, in-group chunk 2(db%4) + (q>>1),
+  // byte 8(q&1) inside the chunk.
+  const int e = l16 >> 2, qq = l16 & 3;
+  const int vsw = swz(4 * g + e);
+  int v_off[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) v_off[d] = (4 * g + e) * 128 + 16 * ((2 * d + (qq >> 1)) ^ vsw) + 8 * (qq & 1);
+  // Partial-score exchange slots: [buffer][wave][j = 2kb + qg][lane] x 16 B.
+  const int x_own = wave * 4096 + lane * 16;
+  const int x_peer = (wave ^ 1) * 4096 + lane * 16;
+
+  // Full scores S^T[key 16kb + 4g + i][query 16qg + l16] of tile t in the exp2 domain, masked.
+  auto scores = [&](int t, float (&x)[2][8]) {
+    const DMLA_LDS char* tb = lds + ((t - tile_begin) % kRing) * kTileBytes;
+    f32x4 sacc[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sacc[kb][0] = sacc[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < kKcHalf; ++c) {
+        constexpr int c0 = kHalf * kKcHalf;
+        const int cc = c0 + c;
+        const int off = k_off[cc & 1] + (cc >> 1) * kGroupBytes + kb * 16 * 128;
+        const bf16x8 a = lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(tb + off));
+        sacc[kb][0] = mfma_bf16(a, qreg[0][c], sacc[kb][0]);
+        sacc[kb][1] = mfma_bf16(a, qreg[1][c], sacc[kb][1]);
+      }
+    }
+    pipeline_schedule<2 * kKcHalf, 1, kPrefetch>();
+    // Sum the two dims halves through LDS.  Both waves add the same two partials (a+b == b+a),
+    // so the pair holds bitwise-identical scores and takes identical softmax decisions.
+    DMLA_LDS char* xb = xbuf + (t & 1) * kXBytes;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<DMLA_LDS f32x4*>(xb + x_own + j * 1024) = sacc[j >> 1][j & 1];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      sacc[j >> 1][j & 1] += *reinterpret_cast<const DMLA_LDS f32x4*>(xb + x_peer + j * 1024);
+    const int key0 = t * kTileN;
+    const bool need_mask = key0 + kTileN - 1 > wg_min_lim;
+#pragma unroll
+    for (int qg = 0; qg < 2; ++qg) {
+      const int lim = need_mask ? limit_of(row_of(qg)) : 0;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float v = sacc[kb][qg][i] * p.scale_log2;
+          if (need_mask) v = key0 + 16 * kb + 4 * g + i > lim ? kNegInf : v;
+          x[qg][kb * 4 + i] = v;
+        }
+    }
+  };
+
+  f32x4 oacc[kDbHalf][2];
+  float mref[2];   // max the accumulators are relative to (fixed once set)
+  float mtrue[2];  // exact running max of this lane's keys
+  float lsum[2];   // this lane's partial row sum relative to mref
+
+  for (int pass = 0; pass < 2; ++pass) {
+    if (pass == 1) {
+      // Exact row max of the whole row tile, then recompute with mref fixed to it.
+      float mx[2] = {kNegInf, kNegInf};
+      if (tile_begin < tile_end) stage(tile_begin);
+      if (tile_begin + 1 < tile_end) stage(tile_begin + 1);
+      for (int t = tile_begin; t < tile_end; ++t) {
+        wait_tile(t);
+        __syncthreads();
+        if (t + 2 < tile_end) stage(t + 2);
+        float x[2][8];
+        scores(t, x);
+#pragma unroll
+        for (int qg = 0; qg < 2; ++qg)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) mx[qg] = fmaxf(mx[qg], x[qg][j]);
+      }
+      wait_vmem();
+      __syncthreads();
+      mref[0] = group_max(mx[0]);
+      mref[1] = group_max(mx[1]);
+    } else {
+      mref[0] = mref[1] = kNegInf;
+    }
+#pragma unroll
+    for (int db = 0; db < kDbHalf; ++db) oacc[db][0] = oacc[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    mtrue[0] = mtrue[1] = kNegInf;
+    lsum[0] = lsum[1] = 0.f;
+    int overflow = 0;
+
+    if (tile_begin < tile_end) stage(tile_begin);
+    if (tile_begin + 1 < tile_end) stage(tile_begin + 1);
+    for (int t = tile_begin; t < tile_end; ++t) {
+      wait_tile(t);
+      if (__syncthreads_or(overflow)) break;
+      if (t + 2 < tile_end) stage(t + 2);
+      const DMLA_LDS char* tb = lds + ((t - tile_begin) % kRing) * kTileBytes;
+      float x[2][8];
+      scores(t, x);
+      float mloc[2];
+#pragma unroll
+      for (int qg = 0; qg < 2; ++qg) {
+        float mx = x[qg][0];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) mx = fmaxf(mx, x[qg][j]);
+        mloc[qg] = mx;
+        mtrue[qg] = fmaxf(mtrue[qg], mx);
+      }
+      // A row seeing its first finite scores adopts the group max as mref (its O and l are
+      // still zero); a row whose scores climb past mref + kHeadroom requests pass 1.
+      const bool unset = (mref[0] == kNegInf && mloc[0] != kNegInf) || (mref[1] == kNegInf && mloc[1] != kNegInf);
+      if (__any(unset)) {
+#pragma unroll
+        for (int qg = 0; qg < 2; ++qg) {
+          const float mt = group_max(mloc[qg]);
+          if (mref[qg] == kNegInf) mref[qg] = mt;
+        }
+      }
+      if (mloc[0] > mref[0] + kHeadroom || mloc[1] > mref[1] + kHeadroom) overflow = 1;
+      bf16x8 pk[2];  // [qg]: keys {4g..4g+3, 16+4g..16+4g+3}
+#pragma unroll
+      for (int qg = 0; qg < 2; ++qg) {
+        const float ms = mref[qg] == kNegInf ? 0.f : mref[qg];
+        float ls = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float pv = fast_exp2(fminf(x[qg][j] - ms, kHeadroom));
+          ls += pv;
+          pk[qg][j] = (bf16)pv;
+        }
+        lsum[qg] += ls;
+      }
+
+      // O^T[dv][query] += V^T . P^T over this wave's half of the output columns.
+#pragma unroll
+      for (int d = 0; d < kDbHalf; ++d) {
+        constexpr int db0 = kHalf * kDbHalf;
+        const int db = db0 + d;
+        const int base = v_off[db & 3] + (db >> 2) * kGroupBytes;
+        const bf16x4 v0 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tb + base));
+        const bf16x4 v1 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tb + base + 16 * 128));
+        const bf16x8 a = concat(v0, v1);
+        oacc[d][0] = mfma_bf16(a, pk[0], oacc[d][0]);
+        oacc[d][1] = mfma_bf16(a, pk[1], oacc[d][1]);
+      }
+      pipeline_schedule<kDbHalf, 2, kPrefetch>();
+    }
+    wait_vmem();
+    if (!__syncthreads_or(overflow)) break;
+  }
+
+  // ---- epilogue ---------------------------------------------------------------------------
+  const bool poison = kDecode && __any(bad_page);
+  const float nanv = __builtin_nanf("");
+#pragma unroll
+  for (int qg = 0; qg < 2; ++qg) {
+    const int r = row_of(qg);
+    const float ltot = group_sum(lsum[qg]);
+    const float mt = group_max(mtrue[qg]);
+    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+    if (r >= nrows) continue;
+    const int col = kHalf * (kDv / 2) + 4 * g;
+    if constexpr (!kDecode) {
+      const int pos = r / p.H, head = r - pos * p.H;
+      bf16* orp = p.o + b * p.o_sb + head * p.o_sh + pos * p.o_ss + col;
+#pragma unroll
+      for (int d = 0; d < kDbHalf; ++d) {
+        const f32x4 v = oacc[d][qg] * inv;
+        bf16x4 w;
+        w[0] = (bf16)v[0]; w[1] = (bf16)v[1]; w[2] = (bf16)v[2]; w[3] = (bf16)v[3];
+        *reinterpret_cast<bf16x4*>(orp + 16 * d) = w;
+      }
+      if (kHalf == 0 && g == 0 && p.m != nullptr) {
+        const int si = (b * p.H + head) * p.Sq + pos;
+        p.m[si] = mt == kNegInf ? kNegInf : mt * kLn2;
+        p.l[si] = mt == kNegInf ? 0.f : ltot * fast_exp2(mref[qg] - mt);
+      }
+    } else {
+      const float lse = poison ? nanv : (ltot > 0.f ? (mref[qg] + __log2f(ltot)) * kLn2 : kNegInf);
+      if (wk.nsplit == 1) {
+        bf16* orp = p.o + b * p.o_sb + r * p.o_sh + col;
+#pragma unroll
+        for (int d = 0; d < kDbHalf; ++d) {
+          f32x4 v = oacc[d][qg] * inv;
+          if (poison) v = f32x4{nanv, nanv, nanv, nanv};
+          bf16x4 w;
+          w[0] = (bf16)v[0]; w[1] = (bf16)v[1]; w[2] = (bf16)v[2]; w[3] = (bf16)v[3];
+          *reinterpret_cast<bf16x4*>(orp + 16 * d) = w;
+        }
+        if (kHalf == 0 && g == 0 && p.lse != nullptr) p.lse[b * p.H + r] = lse;
+      } else {
+        const int64_t slot = ((int64_t)b * p.max_splits + wk.split) * p.H + r;
+        float* pp = p.part_o + slot * kDv + col;
+#pragma unroll
+        for (int d = 0; d < kDbHalf; ++d) {
+          f32x4 v = oacc[d][qg] * inv;
+          if (poison) v = f32x4{nanv, nanv, nanv, nanv};
+          *reinterpret_cast<f32x4*>(pp + 16 * d) = v;
+        }
+        if (kHalf == 0 && g == 0) p.part_lse[slot] = lse;
+      }
+    }
+  }
+}
+
+template <bool kDecode>
+__global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+  DMLA_LDS char* lds = (DMLA_LDS char*)smem;
+  const int lane = lane_id();
+  const int wave = uniform(threadIdx.x >> 6);
+
+  Work wk = {};
+  if constexpr (!kDecode) {
+    // Heaviest (latest) row tiles first; consecutive ids alternate batches so each XCD's L2
+    // sees few distinct K_lat sequences.
+    const int id = blockIdx.x;
+    wk.b = id % p.B;
+    const int rt = p.n_row_tiles - 1 - id / p.B;
+    wk.row0 = rt * kRowsPerWG;
+    const int last_row = min(wk.row0 + kRowsPerWG, p.H * p.Sq) - 1;
+    const int last_pos = last_row / p.H;
+    int kend = p.causal ? min(p.Sk, last_pos + 1 + (p.Sk - p.Sq)) : p.Sk;
+    kend = max(kend, 0);
+    wk.tile_begin = 0;
+    wk.tile_end = (kend + kTileN - 1) / kTileN;
+    wk.nsplit = 1;
+  } else {
+    // Id -> (unit = (b, split), head group) with the head groups of one unit 8 ids apart, so
+    // they run on the same XCD and the second read of the unit's pages hits that XCD's L2.
+    const int id = blockIdx.x;
+    const int hg = (id / 8) % p.head_groups;
+    const int unit = (id / (8 * p.head_groups)) * 8 + id % 8;
+    if (unit >= p.n_units) return;
+    wk.b = unit / p.max_splits;
+    wk.split = unit % p.max_splits;
+    wk.row0 = hg * kRowsPerWG;
+    wk.ctx = min(max(p.seqlens[wk.b], 0), p.max_pages * kPage);
+    const int npages = (wk.ctx + kPage - 1) / kPage;
+    wk.nsplit = max(1, (npages + p.pages_per_split - 1) / p.pages_per_split);
+    if (wk.split >= wk.nsplit) return;
+    wk.page_begin = wk.split * p.pages_per_split;
+    const int page_end = min(npages, wk.page_begin + p.pages_per_split);
+    wk.tile_begin = wk.page_begin * (kPage / kTileN);
+    wk.tile_end = min((wk.ctx + kTileN - 1) / kTileN, page_end * (kPage / kTileN));
+    // Cache this split's page indices in LDS (read by the wave-uniform staging code).
+    DMLA_LDS int* page_cache = reinterpret_cast<DMLA_LDS int*>(lds + kRing * kTileBytes + 2 * kXBytes);
+    for (int i = threadIdx.x; i < page_end - wk.page_begin; i += kThreads)
+      page_cache[i] = p.block_table[wk.b * p.bt_sb + wk.page_begin + i];
+    __syncthreads();
+  }
+  if ((wave & 1) == 0) mqa_fwd_body<kDecode, 0>(p, wk, lds, wave, lane);
+  else mqa_fwd_body<kDecode, 1>(p, wk, lds, wave, lane);
+}
+
+// Merges the normalised split partials of one (sequence, head): o = sum_s w_s o_s / sum_s w_s
+// with w_s = exp(lse_s - max lse).  One 128-thread block per (b, h), 4 columns per thread.
+__global__ __launch_bounds__(128) void decode_combine_kernel(MqaParams p) {
+  const int b = blockIdx.x / p.H, h = blockIdx.x % p.H;
+  const int ctx = min(max(p.seqlens[b], 0), p.max_pages * kPage);
+  const int npages = (ctx + kPage - 1) / kPage;
+  const int nsplit = max(1, (npages + p.pages_per_split - 1) / p.pages_per_split);
+  if (nsplit == 1) return;
+  const int64_t base = (int64_t)b * p.max_splits * p.H + h;
+  float mx = kNegInf;
+  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, p.part_lse[base + (int64_t)s * p.H]);
+  const float mref = mx == kNegInf ? 0.f : mx;
+  float wsum = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const int col = threadIdx.x * 4;
+  for (int s = 0; s < nsplit; ++s) {
+    const int64_t slot = base + (int64_t)s * p.H;
+    const float w = __expf(p.part_lse[slot] - mref);
+    wsum += w;
+    acc += w * *reinterpret_cast<const f32x4*>(p.part_o + slot * kDv + col);
+  }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  acc *= inv;
+  bf16x4 w4;
+  w4[0] = (bf16)acc[0]; w4[1] = (bf16)acc[1]; w4[2] = (bf16)acc[2]; w4[3] = (bf16)acc[3];
+  *reinterpret_cast<bf16x4*>(p.o + b * p.o_sb + h * p.o_sh + col) = w4;
+  if (threadIdx.x == 0 && p.lse != nullptr) p.lse[b * p.H + h] = wsum > 0.f ? mref + __logf(wsum) : mx;
+}
+
+// Pages per split for a decode batch: enough splits to give every CU about two workgroups'
+// worth of pages when all sequences are at full length.
+int decode_pages_per_split(int64_t B, int64_t H, int64_t max_pages) {
+  const int64_t cus = device_cu_count();
+  const int64_t hg = (H + kRowsPerWG - 1) / kRowsPerWG;
+  const int64_t total = B * hg * max_pages;
+  int64_t pps = (total + 2 * cus - 1) / (2 * cus);
+  if (pps < 2) pps = 2;
+  if (pps > max_pages) pps = max_pages;
+  if (pps > kMaxSplitPages) pps = kMaxSplitPages;
+  return (int)(pps < 1 ? 1 : pps);
+}
+
+}  // namespace
+}  // namespace dmla
+
+using namespace dmla;
+
+extern "C" int dmla_fwd_cache_latent(const void* q, const void* k_lat, void* o, float* m, float* l,
+                                     int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t d_qk,
+                                     int64_t d_v, int64_t q_sb, int64_t q_sh, int64_t q_ss,
+                                     int64_t k_sb, int64_t k_ss, int64_t o_sb, int64_t o_sh,
+                                     int64_t o_ss, float softmax_scale, int causal,
+                                     dmla_stream_t stream) {
+  clear_error();
+  if (!q || !k_lat || !o) return fail(DMLA_ERR_INVALID_ARG, "dmla_fwd_cache_latent: null q/k_lat/o");
+  if ((m == nullptr) != (l == nullptr))
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_fwd_cache_latent: m and l must both be set or both be NULL");
+  if (B < 0 || H < 0 || Sq < 0 || Sk < 0)
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_fwd_cache_latent: negative size");
+  if (d_qk != kDqk || d_v != kDv)
+    return fail(DMLA_ERR_UNSUPPORTED, "dmla_fwd_cache_latent: only d_qk=576, d_v=512 is compiled (got %lld, %lld)",
+                (long long)d_qk, (long long)d_v);
+  if (!(softmax_scale > 0.f) || !__builtin_isfinite(softmax_scale))
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_fwd_cache_latent: softmax_scale must be finite and > 0");
+  if (!aligned16(q) || !aligned16(k_lat) || !aligned16(o))
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_fwd_cache_latent: q/k_lat/o must be 16-byte aligned");
+  if (!mult8(q_sb) || !mult8(q_sh) || !mult8(q_ss) || !mult8(k_sb) || !mult8(k_ss) || !mult8(o_sb) ||
+      !mult8(o_sh) || !mult8(o_ss))
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_fwd_cache_latent: strides must be multiples of 8 elements");
+  if (k_ss < kDqk || k_ss * 2 * kTileN >= ((int64_t)1 << 31))
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_fwd_cache_latent: k_lat row stride out of range");
+  const int64_t rows = H * Sq;
+  if (rows > ((int64_t)1 << 30) || Sk > ((int64_t)1 << 30))
+    return fail(DMLA_ERR_UNSUPPORTED, "dmla_fwd_cache_latent: size too large");
+  if (B == 0 || rows == 0) return DMLA_OK;
+
+  MqaParams p = {};
+  p.q = static_cast<const bf16*>(q);
+  p.kv = static_cast<const bf16*>(k_lat);
+  p.o = static_cast<bf16*>(o);
+  p.m = m;
+  p.l = l;
+  p.q_sb = q_sb; p.q_sh = q_sh; p.q_ss = q_ss;
+  p.k_sb = k_sb; p.k_ss = k_ss;
+  p.o_sb = o_sb; p.o_sh = o_sh; p.o_ss = o_ss;
+  p.B = (int)B; p.H = (int)H; p.Sq = (int)Sq; p.Sk = (int)Sk;
+  p.scale_log2 = softmax_scale * kLog2e;
+  p.causal = causal ? 1 : 0;
+  p.n_row_tiles = (int)((rows + kRowsPerWG - 1) / kRowsPerWG);
+  const int64_t grid = (int64_t)p.n_row_tiles * B;
+  if (grid > 0x7fffffff) return fail(DMLA_ERR_UNSUPPORTED, "dmla_fwd_cache_latent: grid too large");
+  hipLaunchKernelGGL(mqa_fwd_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0,
+                     (hipStream_t)stream, p);
+  return check_launch("dmla_fwd_cache_latent");
+}
+
+extern "C" int64_t dmla_decode_workspace_bytes(int64_t B, int64_t H, int64_t d_v, int64_t max_pages_per_seq) {
+  if (B <= 0 || H <= 0 || d_v != kDv || max_pages_per_seq <= 0) return 0;
+  const int pps = decode_pages_per_split(B, H, max_pages_per_seq);
+  const int64_t max_splits = (max_pages_per_seq + pps - 1) / pps;
+  if (max_splits <= 1) return 0;
+  return B * max_splits * H * (int64_t)(kDv + 1) * (int64_t)sizeof(float);
+}
+
+extern "C" int dmla_decode_paged(const void* q, const void* kv_pool, const int32_t* block_table,
+                                 const int32_t* cache_seqlens, void* o, float* lse, int64_t B,
+                                 int64_t H, int64_t d_qk, int64_t d_v, int64_t page_size,
+                                 int64_t num_pages, int64_t max_pages_per_seq, int64_t q_sb,
+                                 int64_t q_sh, int64_t kv_sp, int64_t kv_ss, int64_t bt_sb,
+                                 int64_t o_sb, int64_t o_sh, float softmax_scale, void* workspace,
+                                 int64_t workspace_bytes, dmla_stream_t stream) {
+  clear_error();
+  if (!q || !kv_pool || !block_table || !cache_seqlens || !o)
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: null pointer argument");
+  if (B < 0 || H < 0 || num_pages < 0 || max_pages_per_seq < 0)
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: negative size");
+  if (d_qk != kDqk || d_v != kDv || page_size != kPage)
+    return fail(DMLA_ERR_UNSUPPORTED, "dmla_decode_paged: only d_qk=576, d_v=512, page_size=64 is compiled (got %lld, %lld, %lld)",
+                (long long)d_qk, (long long)d_v, (long long)page_size);
+  if (!(softmax_scale > 0.f) || !__builtin_isfinite(softmax_scale))
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: softmax_scale must be finite and > 0");
+  if (!aligned16(q) || !aligned16(kv_pool) || !aligned16(o))
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: q/kv_pool/o must be 16-byte aligned");
+  if (!mult8(q_sb) || !mult8(q_sh) || !mult8(kv_sp) || !mult8(kv_ss) || !mult8(o_sb) || !mult8(o_sh))
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: strides must be multiples of 8 elements");
+  if (kv_ss < kDqk || kv_sp < kv_ss * kPage || kv_ss * 2 * kPage >= ((int64_t)1 << 31))
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: kv_pool strides out of range");
+  if (bt_sb < max_pages_per_seq)
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: block_table row stride %lld < max_pages_per_seq %lld",
+                (long long)bt_sb, (long long)max_pages_per_seq);
+  if (H > ((int64_t)1 << 16) || B > ((int64_t)1 << 20) || max_pages_per_seq > ((int64_t)1 << 24) ||
+      num_pages > 0x7fffffff)
+    return fail(DMLA_ERR_UNSUPPORTED, "dmla_decode_paged: size too large");
+  if (B == 0 || H == 0) return DMLA_OK;
+  if (num_pages == 0 || max_pages_per_seq == 0)
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: empty page pool or block table");
+
+  MqaParams p = {};
+  p.q = static_cast<const bf16*>(q);
+  p.kv = static_cast<const bf16*>(kv_pool);
+  p.o = static_cast<bf16*>(o);
+  p.lse = lse;
+  p.q_sb = q_sb; p.q_sh = q_sh;
+  p.k_sb = kv_sp; p.k_ss = kv_ss;
+  p.o_sb = o_sb; p.o_sh = o_sh;
+  p.B = (int)B; p.H = (int)H; p.Sq = 1; p.Sk = 0;
+  p.scale_log2 = softmax_scale * kLog2e;
+  p.block_table = block_table;
+  p.seqlens = cache_seqlens;
+  p.bt_sb = bt_sb;
+  p.num_pages = (int)num_pages;
+  p.max_pages = (int)max_pages_per_seq;
+  p.pages_per_split = decode_pages_per_split(B, H, max_pages_per_seq);
+  p.max_splits = (int)((max_pages_per_seq + p.pages_per_split - 1) / p.pages_per_split);
+  p.head_groups = (int)((H + kRowsPerWG - 1) / kRowsPerWG);
+  p.n_units = (int)(B * p.max_splits);
+  if (p.max_splits > 1) {
+    const int64_t need = dmla_decode_workspace_bytes(B, H, d_v, max_pages_per_seq);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(DMLA_ERR_WORKSPACE, "dmla_decode_paged: workspace of %lld bytes needed (got %lld)",
+                  (long long)need, (long long)workspace_bytes);
+    if (!aligned16(workspace)) return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: workspace must be 16-byte aligned");
+    p.part_o = static_cast<float*>(workspace);
+    p.part_lse = p.part_o + B * p.max_splits * H * kDv;
+  }
+  const int64_t grid = (((int64_t)p.n_units + 7) / 8) * 8 * p.head_groups;
+  if (grid > 0x7fffffff) return fail(DMLA_ERR_UNSUPPORTED, "dmla_decode_paged: grid too large");
+  hipLaunchKernelGGL(mqa_fwd_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream, p);
+  int rc = check_launch("dmla_decode_paged");
+  if (rc != DMLA_OK || p.max_splits == 1) return rc;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(B * H)), dim3(kDv / 4), 0, (hipStream_t)stream, p);
+  return check_launch("dmla_decode_paged(combine)");
+}

@@ -1,0 +1,45 @@
+// Error state and small host utilities behind the C ABI.
+#include <cstdarg>
+#include <cstdio>
+
+#include "dmla_host.h"
+
+namespace dmla {
+
+namespace {
+thread_local char g_msg[512] = {0};
+}
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_msg, sizeof(g_msg), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_error() { g_msg[0] = 0; }
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(DMLA_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return DMLA_OK;
+}
+
+int device_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+}  // namespace dmla
+
+extern "C" int dmla_version(void) { return 100; /* 0.1.0 */ }
+
+extern "C" const char* dmla_last_error(void) { return dmla::g_msg; }

@@ -1,0 +1,12 @@
+"""Flash-DMLA for MI355X (gfx950): Python API over the HIP kernels in libflashdmla.so."""
+from .ops import (  # noqa: F401
+    D_QK,
+    D_V,
+    PAGE_SIZE,
+    FlashDMLACacheLatent,
+    flash_dmla,
+    flash_dmla_bwd,
+    flash_dmla_decode_paged,
+    flash_dmla_fwd,
+)
+from ._lib import DmlaError, DmlaInvalidArgument, DmlaUnsupported  # noqa: F401

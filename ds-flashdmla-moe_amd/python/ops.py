@@ -1,0 +1,180 @@
+"""Flash-DMLA operators: ``torch.autograd.Function`` wrappers over the gfx950 HIP kernels.
+
+This is the Python API the reference's README promises ("minimal autograd.Function wrappers",
+README.md:25 and the absent python/ops.py of README.md:54-56).  Every op calls
+``libflashdmla.so`` through its C ABI on the current HIP stream; there is no CPU or PyTorch
+fallback -- a missing library or a non-GPU tensor raises.
+
+Conventions (the reference fixes none of them; see the oracle for the restated math):
+  * q [B, H, S, 576] bf16 and a head-shared latent cache k_lat [B, S_k, 576] bf16; V_lat is
+    k_lat[..., :d_v] with d_v = 512.
+  * softmax_scale defaults to 1/sqrt(d_qk).
+  * causal masks key j > i + (S_k - S_q) (bottom-right aligned; j > i when S_q == S_k).
+  * m, l are the row max and row sum in natural-log units of the scaled scores
+    (m = max_j scale*q.k_j, l = sum_j exp(scale*q.k_j - m)), as in fa_fwd.cu:81-123.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+D_QK = 576
+D_V = 512
+PAGE_SIZE = 64
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t: Optional[torch.Tensor]) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _check_bf16(name: str, t: torch.Tensor, ndim: int) -> None:
+    _require(isinstance(t, torch.Tensor), f"{name} must be a tensor")
+    _require(t.is_cuda, f"{name} must be a GPU tensor (the HIP kernels have no CPU path)")
+    _require(t.dtype == torch.bfloat16, f"{name} must be bfloat16, got {t.dtype}")
+    _require(t.dim() == ndim, f"{name} must have {ndim} dims, got shape {tuple(t.shape)}")
+    _require(t.stride(-1) == 1, f"{name} must be contiguous in its last dim")
+
+
+def _scale(softmax_scale: Optional[float], d_qk: int) -> float:
+    return float(softmax_scale) if softmax_scale is not None else 1.0 / math.sqrt(d_qk)
+
+
+def flash_dmla_fwd(
+    q: torch.Tensor,
+    k_lat: torch.Tensor,
+    d_v: int = D_V,
+    softmax_scale: Optional[float] = None,
+    causal: bool = True,
+    return_stats: bool = True,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor]]:
+    """Cache-latent DMLA forward: returns (o [B,H,Sq,d_v] bf16, m, l [B,H,Sq] fp32).
+
+    o[b,h,i] = softmax(scale * q[b,h,i] . k_lat[b]^T (+ causal mask)) . k_lat[b][:, :d_v].
+    """
+    _check_bf16("q", q, 4)
+    _check_bf16("k_lat", k_lat, 3)
+    B, H, Sq, Dqk = q.shape
+    _require(k_lat.shape[0] == B and k_lat.shape[2] == Dqk,
+             f"k_lat shape {tuple(k_lat.shape)} does not match q {tuple(q.shape)}")
+    _require(q.device == k_lat.device, "q and k_lat must be on the same device")
+    Sk = k_lat.shape[1]
+    o = torch.empty((B, H, Sq, d_v), dtype=torch.bfloat16, device=q.device)
+    m = l = None
+    if return_stats:
+        m = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device)
+        l = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device)
+    _lib.call(
+        "dmla_fwd_cache_latent",
+        _ptr(q), _ptr(k_lat), _ptr(o), _ptr(m), _ptr(l),
+        B, H, Sq, Sk, Dqk, d_v,
+        q.stride(0), q.stride(1), q.stride(2),
+        k_lat.stride(0), k_lat.stride(1),
+        o.stride(0), o.stride(1), o.stride(2),
+        _scale(softmax_scale, Dqk), 1 if causal else 0, _stream(q),
+    )
+    return o, m, l
+
+
+def flash_dmla_decode_paged(
+    q: torch.Tensor,
+    kv_pool: torch.Tensor,
+    block_table: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    d_v: int = D_V,
+    softmax_scale: Optional[float] = None,
+    return_lse: bool = False,
+    check_indices: bool = False,
+):
+    """Paged-KV DMLA decode for one query token per sequence.
+
+    q [B, H, 576] bf16; kv_pool [num_pages, 64, 576] bf16; block_table [B, max_pages] int32;
+    cache_seqlens [B] int32.  Returns o [B, H, d_v] bf16 (and lse [B, H] fp32 natural log when
+    return_lse).  Token t of sequence b is kv_pool[block_table[b, t // 64], t % 64].
+    check_indices=True validates the table and lengths on the host (one device sync) and raises
+    instead of producing NaN rows for out-of-range pages.
+    """
+    _check_bf16("q", q, 3)
+    _check_bf16("kv_pool", kv_pool, 3)
+    _require(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.is_cuda,
+             "block_table must be a 2-D int32 GPU tensor")
+    _require(block_table.stride(1) == 1, "block_table must be contiguous in its last dim")
+    _require(cache_seqlens.dtype == torch.int32 and cache_seqlens.dim() == 1 and cache_seqlens.is_cuda,
+             "cache_seqlens must be a 1-D int32 GPU tensor")
+    _require(cache_seqlens.is_contiguous(), "cache_seqlens must be contiguous")
+    B, H, Dqk = q.shape
+    num_pages, page, Dk = kv_pool.shape
+    _require(Dk == Dqk, f"kv_pool last dim {Dk} != q last dim {Dqk}")
+    _require(page == PAGE_SIZE, f"page size must be {PAGE_SIZE}, got {page}")
+    _require(block_table.shape[0] == B and cache_seqlens.shape[0] == B, "batch size mismatch")
+    max_pages = block_table.shape[1]
+    if check_indices:
+        bt = block_table.cpu()
+        sl = cache_seqlens.cpu()
+        _require(bool((sl >= 0).all()), "cache_seqlens must be >= 0")
+        _require(int(sl.max()) <= max_pages * PAGE_SIZE if B else True,
+                 "a cache_seqlens entry exceeds the block table capacity")
+        for b in range(B):
+            n = (int(sl[b]) + PAGE_SIZE - 1) // PAGE_SIZE
+            used = bt[b, :n]
+            _require(bool(((used >= 0) & (used < num_pages)).all()),
+                     f"block_table row {b} holds a page index outside [0, {num_pages})")
+    o = torch.empty((B, H, d_v), dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty((B, H), dtype=torch.float32, device=q.device) if return_lse else None
+    ws_bytes = int(_lib.lib().dmla_decode_workspace_bytes(B, H, d_v, max_pages))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
+    _lib.call(
+        "dmla_decode_paged",
+        _ptr(q), _ptr(kv_pool), _ptr(block_table), _ptr(cache_seqlens), _ptr(o), _ptr(lse),
+        B, H, Dqk, d_v, page, num_pages, max_pages,
+        q.stride(0), q.stride(1), kv_pool.stride(0), kv_pool.stride(1), block_table.stride(0),
+        o.stride(0), o.stride(1),
+        _scale(softmax_scale, Dqk), _ptr(ws), ws_bytes, _stream(q),
+    )
+    return (o, lse) if return_lse else o
+
+
+class FlashDMLACacheLatent(torch.autograd.Function):
+    """o = FlashDMLACacheLatent.apply(q, k_lat, d_v, softmax_scale, causal).
+
+    Saves (q, k_lat, o, m, l) for the backward, which reuses the row statistics instead of
+    recomputing them (README.md:12).
+    """
+
+    @staticmethod
+    def forward(ctx, q, k_lat, d_v=D_V, softmax_scale=None, causal=True):
+        o, m, l = flash_dmla_fwd(q, k_lat, d_v, softmax_scale, causal, return_stats=True)
+        ctx.save_for_backward(q, k_lat, o, m, l)
+        ctx.d_v = d_v
+        ctx.softmax_scale = softmax_scale
+        ctx.causal = causal
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k_lat, o, m, l = ctx.saved_tensors
+        dq, dk_lat = flash_dmla_bwd(q, k_lat, o, do, m, l, ctx.d_v, ctx.softmax_scale, ctx.causal)
+        return dq, dk_lat, None, None, None
+
+
+def flash_dmla_bwd(q, k_lat, o, do, m, l, d_v=D_V, softmax_scale=None, causal=True):
+    """Cache-latent DMLA backward from the saved statistics: returns (dq, dk_lat)."""
+    raise NotImplementedError("flash_dmla_bwd: the backward kernel is not built into this library yet")
+
+
+def flash_dmla(q, k_lat, d_v=D_V, softmax_scale=None, causal=True):
+    """Differentiable cache-latent DMLA attention (functional form of FlashDMLACacheLatent)."""
+    return FlashDMLACacheLatent.apply(q, k_lat, d_v, softmax_scale, causal)

@@ -1,0 +1,101 @@
+/*
+ * flashdmla.h -- C ABI of the MI355X-native Flash-DMLA attention backend (gfx950).
+ *
+ * Every entry point:
+ *   - takes caller-owned device pointers and explicit element strides (the last dimension of
+ *     every bf16 tensor must be contiguous and 16-byte aligned);
+ *   - is asynchronous and stream-ordered on `stream` (a hipStream_t; NULL = default stream);
+ *   - allocates nothing: scratch memory is a caller-provided `workspace` whose size comes from
+ *     the matching *_workspace_bytes() query;
+ *   - returns DMLA_OK (0) or a negative status; dmla_last_error() then describes the failure.
+ *
+ * The reference's launchers (e.g. `fa2_forward`, csrc/attention/fa2_fwd.cu:139-156) take
+ * `(const float* Q, const float* K, const float* V, float* O, int Nq, int Nk, int d, int dv,
+ *  float scale, int warps_per_block, cudaStream_t)` and return void, silently doing nothing on
+ * bad arguments (fa2_fwd.cu:149).  The entry points below keep that calling pattern --
+ * raw pointers, sizes, scale, stream -- and add batch/head strides, bf16 storage, the saved
+ * softmax statistics of README.md:12 and an error status.
+ *
+ * Element types: `bf16` tensors are passed as `const void*` holding IEEE bfloat16 values;
+ * statistics are fp32; page tables and sequence lengths are int32.
+ */
+#ifndef FLASHDMLA_H
+#define FLASHDMLA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DMLA_OK 0
+#define DMLA_ERR_INVALID_ARG (-1)  /* null pointer, bad shape, stride or alignment */
+#define DMLA_ERR_UNSUPPORTED (-2)  /* a shape outside the compiled kernel family */
+#define DMLA_ERR_WORKSPACE (-3)    /* workspace missing or too small */
+#define DMLA_ERR_HIP (-4)          /* the HIP runtime reported an error at launch */
+
+typedef void* dmla_stream_t; /* hipStream_t */
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int dmla_version(void);
+
+/* Message for the most recent failing call on this host thread ("" if none). */
+const char* dmla_last_error(void);
+
+/*
+ * Cache-latent DMLA forward (prefill).
+ * Replaces: fa2_forward (csrc/attention/fa2_fwd.cu:139-156) specialised to the cache-latent
+ * mode of README.md:15 -- the role of the absent csrc/attention/fa2_dmla_fwd.cu
+ * (README.md:45).
+ *
+ *   q     [B, H, Sq, d_qk] bf16    strides (q_sb, q_sh, q_ss)
+ *   k_lat [B, Sk, d_qk]    bf16    strides (k_sb, k_ss); shared by all H heads;
+ *                                  V_lat is k_lat[..., :d_v]
+ *   o     [B, H, Sq, d_v]  bf16    strides (o_sb, o_sh, o_ss)
+ *   m, l  [B, H, Sq]       fp32    contiguous; may both be NULL (statistics not written)
+ *
+ *   m[b,h,i] = max_j s_ij and l[b,h,i] = sum_j exp(s_ij - m[b,h,i]) over unmasked keys j, with
+ *   s_ij = softmax_scale * q_i . k_j (natural-log units, the recurrence of fa_fwd.cu:81-123).
+ *   causal != 0 masks key j > i + (Sk - Sq).  A row with no unmasked key gets o = 0,
+ *   m = -inf, l = 0 (the 1/l guard of fa_fwd.cu:117-118).
+ *
+ * Supported: d_qk = 576, d_v = 512 (DeepSeek-V3 absorbed latent shape).
+ */
+int dmla_fwd_cache_latent(const void* q, const void* k_lat, void* o, float* m, float* l,
+                          int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t d_qk,
+                          int64_t d_v, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t k_sb,
+                          int64_t k_ss, int64_t o_sb, int64_t o_sh, int64_t o_ss,
+                          float softmax_scale, int causal, dmla_stream_t stream);
+
+/*
+ * Paged-KV DMLA decode (one query token per sequence).
+ * No reference counterpart exists (the reference has no paged decode); it is the decode form
+ * of fa2_forward (fa2_fwd.cu:139-156) over the latent cache.
+ *
+ *   q             [B, H, d_qk]                 bf16  strides (q_sb, q_sh)
+ *   kv_pool       [num_pages, page_size, d_qk] bf16  strides (kv_sp, kv_ss); V = [..., :d_v]
+ *   block_table   [B, max_pages_per_seq]       int32 row stride bt_sb; entries in [0, num_pages)
+ *   cache_seqlens [B]                          int32 context length of each sequence
+ *   o             [B, H, d_v]                  bf16  strides (o_sb, o_sh)
+ *   lse           [B, H]                       fp32  contiguous, natural log; may be NULL
+ *
+ * Sequence b attends its first cache_seqlens[b] tokens; token t lives in page
+ * block_table[b, t / page_size] at row t % page_size.  Lengths above
+ * max_pages_per_seq * page_size are clamped to it.  A page index outside [0, num_pages) is
+ * never dereferenced: the sequence's output and lse are set to NaN instead.
+ * Supported: d_qk = 576, d_v = 512, page_size = 64.
+ */
+int64_t dmla_decode_workspace_bytes(int64_t B, int64_t H, int64_t d_v, int64_t max_pages_per_seq);
+int dmla_decode_paged(const void* q, const void* kv_pool, const int32_t* block_table,
+                      const int32_t* cache_seqlens, void* o, float* lse, int64_t B, int64_t H,
+                      int64_t d_qk, int64_t d_v, int64_t page_size, int64_t num_pages,
+                      int64_t max_pages_per_seq, int64_t q_sb, int64_t q_sh, int64_t kv_sp,
+                      int64_t kv_ss, int64_t bt_sb, int64_t o_sb, int64_t o_sh,
+                      float softmax_scale, void* workspace, int64_t workspace_bytes,
+                      dmla_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHDMLA_H */

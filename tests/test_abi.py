@@ -1,0 +1,100 @@
+"""The C ABI (include/flashdmla.h): the library loads, exports every declared entry point and
+rejects bad arguments with a status and message -- all without touching a GPU.
+
+Every call below returns before any kernel launch (argument errors, missing workspace or an
+empty problem), so the fake device pointers are never dereferenced."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+from python import _lib, ops
+
+HEADER = os.path.join(ROOT, "include", "flashdmla.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dmla_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = declared_functions()
+    assert "dmla_fwd_cache_latent" in names and "dmla_decode_paged" in names
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in flashdmla.h but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature in python/_lib.py"
+    assert lib.dmla_version() >= 100
+
+
+def _fwd(**kw):
+    args = dict(q=1 << 20, k=1 << 20, o=1 << 20, m=None, l=None, B=1, H=16, Sq=8, Sk=8, dqk=576, dv=512,
+                scale=0.07, causal=1)
+    args.update(kw)
+    P = ctypes.c_void_p
+    return _lib.lib().dmla_fwd_cache_latent(
+        P(args["q"]), P(args["k"]), P(args["o"]), P(args["m"]), P(args["l"]),
+        args["B"], args["H"], args["Sq"], args["Sk"], args["dqk"], args["dv"],
+        16 * 8 * 576, 8 * 576, 576, 8 * 576, 576, 16 * 8 * 512, 8 * 512, 512,
+        args["scale"], args["causal"], None)
+
+
+def test_fwd_argument_errors():
+    assert _fwd(q=None) == _lib.DMLA_ERR_INVALID_ARG
+    assert b"null" in _lib.lib().dmla_last_error()
+    assert _fwd(dqk=64, dv=32) == _lib.DMLA_ERR_UNSUPPORTED
+    assert _fwd(scale=-1.0) == _lib.DMLA_ERR_INVALID_ARG
+    assert _fwd(scale=float("inf")) == _lib.DMLA_ERR_INVALID_ARG
+    assert _fwd(q=(1 << 20) + 2) == _lib.DMLA_ERR_INVALID_ARG  # misaligned
+    assert _fwd(m=1 << 20) == _lib.DMLA_ERR_INVALID_ARG        # m without l
+    assert _fwd(B=-1) == _lib.DMLA_ERR_INVALID_ARG
+    # Empty problems succeed without launching anything.
+    assert _fwd(B=0) == _lib.DMLA_OK
+    assert _fwd(Sq=0) == _lib.DMLA_OK
+    assert _lib.lib().dmla_last_error() == b""
+
+
+def test_decode_argument_errors():
+    P = ctypes.c_void_p
+    lib = _lib.lib()
+
+    def call(**kw):
+        a = dict(q=1 << 20, kv=1 << 20, bt=1 << 20, sl=1 << 20, o=1 << 20, B=2, H=128, dqk=576, dv=512,
+                 page=64, num_pages=10, max_pages=4, bt_sb=4, ws=None, ws_bytes=0)
+        a.update(kw)
+        return lib.dmla_decode_paged(P(a["q"]), P(a["kv"]), P(a["bt"]), P(a["sl"]), P(a["o"]), None,
+                                     a["B"], a["H"], a["dqk"], a["dv"], a["page"], a["num_pages"], a["max_pages"],
+                                     128 * 576, 576, 64 * 576, 576, a["bt_sb"], 128 * 512, 512, 0.07,
+                                     P(a["ws"]), a["ws_bytes"], None)
+
+    assert call(bt=None) == _lib.DMLA_ERR_INVALID_ARG
+    assert call(page=32) == _lib.DMLA_ERR_UNSUPPORTED
+    assert call(bt_sb=2) == _lib.DMLA_ERR_INVALID_ARG
+    assert call(num_pages=0) == _lib.DMLA_ERR_INVALID_ARG
+    assert call(B=0) == _lib.DMLA_OK
+    need = lib.dmla_decode_workspace_bytes(64, 128, 512, 128)
+    assert need > 0
+    assert call(B=64, max_pages=128, bt_sb=128) == _lib.DMLA_ERR_WORKSPACE
+
+
+def test_python_wrappers_reject_cpu_tensors_and_bad_shapes():
+    q = torch.zeros(1, 16, 8, 576, dtype=torch.bfloat16)
+    k = torch.zeros(1, 8, 576, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        ops.flash_dmla_fwd(q, k)
+    with pytest.raises(ValueError):
+        ops.flash_dmla_fwd(q.float(), k)
+    with pytest.raises(ValueError):
+        ops.flash_dmla_decode_paged(q[:, :, 0], k, torch.zeros(1, 1, dtype=torch.int32),
+                                    torch.ones(1, dtype=torch.int32))
+
+
+def test_error_message_is_raised_as_exception():
+    with pytest.raises(_lib.DmlaUnsupported, match="576"):
+        _lib.check("dmla_fwd_cache_latent", _fwd(dqk=64, dv=32))

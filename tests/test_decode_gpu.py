@@ -1,0 +1,99 @@
+"""Parity of the paged decode kernel (dmla_decode_paged) with the fp32 oracle."""
+import math
+
+import pytest
+import torch
+
+from conftest import assert_out_close, seeded
+from oracle import dmla_ref as R
+from python import ops
+
+SCALE = 1.0 / math.sqrt(192.0)
+
+
+def _paged(lens, H, seed, page=64, extra_pages=0, poison_tail=True):
+    """Seeded q, a randomly permuted page pool and its block table for the given lengths."""
+    B = len(lens)
+    n_pages = [(n + page - 1) // page for n in lens]
+    total = sum(n_pages) + extra_pages
+    max_pages = max(max(n_pages), 1)
+    g = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(total, generator=g)
+    pool = (torch.randn(total, page, 576, generator=g) * 0.5).to(torch.bfloat16)
+    if poison_tail:
+        # Rows past each sequence's end hold NaN: the kernel must never let them reach o.
+        pool_tail = torch.full((page, 576), float("nan")).to(torch.bfloat16)
+    table = torch.zeros(B, max_pages, dtype=torch.int32)
+    c = 0
+    for b in range(B):
+        for j in range(n_pages[b]):
+            table[b, j] = int(perm[c])
+            c += 1
+        if poison_tail and lens[b] % page:
+            last = int(table[b, n_pages[b] - 1])
+            pool[last, lens[b] % page:] = pool_tail[lens[b] % page:]
+    q = (torch.randn(B, H, 576, generator=g) * 0.5).to(torch.bfloat16)
+    return q, pool, table, torch.tensor(lens, dtype=torch.int32)
+
+
+def _check(gpu, q, pool, table, lens, oracle_device="cpu"):
+    o, lse = ops.flash_dmla_decode_paged(q.to(gpu), pool.to(gpu), table.to(gpu), lens.to(gpu),
+                                         512, SCALE, return_lse=True)
+    torch.cuda.synchronize()
+    dev = gpu if oracle_device == "gpu" else "cpu"
+    o_ref, lse_ref = R.dmla_decode_paged(q.to(dev).float(), pool.to(dev).float(), table.to(dev),
+                                         lens.to(dev), 512, SCALE)
+    assert_out_close(o, o_ref)
+    d = (lse - lse_ref.to(lse.device)).abs().max().item()
+    assert d <= 1e-3, f"lse max-abs {d:.3e}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize(
+    "lens,H",
+    [
+        ([1, 63, 64, 65, 130], 128),   # 1-token context, partial and exact pages
+        ([700, 5, 2048], 128),         # long enough to split across workgroups
+        ([100, 33], 16),               # fewer heads than a workgroup
+        ([256, 257, 300], 96),         # two head groups, the second partial
+    ],
+)
+def test_decode_small(gpu, lens, H):
+    q, pool, table, sl = _paged(lens, H, seed=sum(lens) + H)
+    _check(gpu, q, pool, table, sl)
+
+
+@pytest.mark.gpu
+def test_decode_page_order_does_not_matter(gpu):
+    q, pool, table, sl = _paged([500, 333], 128, seed=11)
+    o1 = ops.flash_dmla_decode_paged(q.to(gpu), pool.to(gpu), table.to(gpu), sl.to(gpu), 512, SCALE)
+    # Move every page to a new physical slot and rewrite the table accordingly.
+    perm = torch.randperm(pool.shape[0], generator=torch.Generator().manual_seed(3))
+    pool2 = torch.empty_like(pool)
+    pool2[perm] = pool
+    table2 = perm[table.long()].to(torch.int32)
+    o2 = ops.flash_dmla_decode_paged(q.to(gpu), pool2.to(gpu), table2.to(gpu), sl.to(gpu), 512, SCALE)
+    assert torch.equal(o1, o2)
+
+
+@pytest.mark.gpu
+def test_decode_bad_page_index_gives_nan_not_a_fault(gpu):
+    q, pool, table, sl = _paged([128, 128], 128, seed=12)
+    table[1, 1] = pool.shape[0] + 5  # out of range: must not be dereferenced
+    o = ops.flash_dmla_decode_paged(q.to(gpu), pool.to(gpu), table.to(gpu), sl.to(gpu), 512, SCALE)
+    torch.cuda.synchronize()
+    assert torch.isnan(o[1].float()).all()
+    assert torch.isfinite(o[0].float()).all()
+    with pytest.raises(ValueError, match="page index"):
+        ops.flash_dmla_decode_paged(q.to(gpu), pool.to(gpu), table.to(gpu), sl.to(gpu), 512, SCALE,
+                                    check_indices=True)
+
+
+@pytest.mark.gpu
+def test_decode_config3_full_shape(gpu):
+    # B=64, H=128, contexts uniform in [1024, 8192], 64-token pages in a
+    # seeded random permutation.
+    g = torch.Generator().manual_seed(3)
+    lens = torch.randint(1024, 8193, (64,), generator=g).tolist()
+    q, pool, table, sl = _paged(lens, 128, seed=3, poison_tail=False)
+    _check(gpu, q, pool, table, sl, oracle_device="gpu")

@@ -1,0 +1,222 @@
+"""Pins the CPU oracle (oracle/dmla_ref.py) before any kernel is compared against it.
+
+Each oracle function is checked against something that does not restate its own formula:
+the golden fixture of config 1 (brute-force fp64 row loops + torch.autograd), a library
+routine (scaled_dot_product_attention, torch.autograd, gradcheck), closed forms and
+invariants.  The planted-mistake tests at the end show that these checks reject plausible
+errors (a dropped scale, a wrong V slice, a transposed operand, a missing V-fold).
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import seeded
+from oracle import dmla_ref as R
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "cfg1_tiny.npz")
+
+
+def _golden():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+# ---------------------------------------------------------------- golden fixture (config 1)
+def test_golden_forward_cfg1():
+    g = _golden()
+    q, k = torch.from_numpy(g["q"]), torch.from_numpy(g["k_lat"])
+    o, m, l = R.dmla_fwd_cache_latent(q, k, int(g["d_v"]), float(g["scale"]), True, torch.float32)
+    np.testing.assert_allclose(o.numpy(), g["o"], atol=2e-6, rtol=1e-5)
+    np.testing.assert_allclose(m.numpy(), g["m"], atol=2e-6, rtol=1e-6)
+    np.testing.assert_allclose(l.numpy(), g["l"], atol=0, rtol=2e-6)
+
+
+def test_golden_forward_cfg1_fp64_tight():
+    g = _golden()
+    q, k = torch.from_numpy(g["q"]).double(), torch.from_numpy(g["k_lat"]).double()
+    o, m, l = R.dmla_fwd_cache_latent(q, k, 32, 1 / 8, True, torch.float64)
+    np.testing.assert_allclose(o.numpy(), g["o"], atol=1e-6, rtol=1e-6)
+    np.testing.assert_allclose((m + torch.log(l)).numpy(), g["lse"], atol=1e-6, rtol=0)
+
+
+def test_golden_backward_cfg1():
+    g = _golden()
+    q, k, do = (torch.from_numpy(g[n]).double() for n in ("q", "k_lat", "do"))
+    o, m, l = R.dmla_fwd_cache_latent(q, k, 32, 1 / 8, True, torch.float64)
+    dq, dk = R.dmla_bwd_cache_latent(q, k, o, do, m, l, 32, 1 / 8, True, torch.float64)
+    np.testing.assert_allclose(dq.numpy(), g["dq"], atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(dk.numpy(), g["dk_lat"], atol=1e-5, rtol=1e-5)
+
+
+# ---------------------------------------------------------------- library cross-checks
+@pytest.mark.parametrize("sq,sk,causal", [(37, 37, True), (16, 53, True), (29, 41, False)])
+def test_forward_matches_sdpa(sq, sk, causal):
+    B, H, D, DV = 2, 3, 40, 24
+    q = seeded((B, H, sq, D), 1, dtype=torch.float64)
+    k = seeded((B, sk, D), 2, dtype=torch.float64)
+    scale = 0.3
+    o, m, l = R.dmla_fwd_cache_latent(q, k, DV, scale, causal, torch.float64)
+    mask = None
+    if causal:
+        mask = ~R.causal_mask(sq, sk)  # True = attend (bottom-right aligned)
+    ref = F.scaled_dot_product_attention(
+        q, k.unsqueeze(1).expand(B, H, sk, D), k[..., :DV].unsqueeze(1).expand(B, H, sk, DV),
+        attn_mask=mask, scale=scale)
+    torch.testing.assert_close(o, ref, atol=1e-12, rtol=1e-12)
+    s = scale * torch.einsum("bhid,bjd->bhij", q, k)
+    if causal:
+        s = s.masked_fill(R.causal_mask(sq, sk), float("-inf"))
+    torch.testing.assert_close(m + torch.log(l), torch.logsumexp(s, -1), atol=1e-12, rtol=1e-12)
+    torch.testing.assert_close(m, s.amax(-1), atol=0, rtol=0)
+
+
+def test_backward_matches_autograd_and_gradcheck():
+    B, H, S, D, DV = 2, 2, 11, 12, 8
+    q = seeded((B, H, S, D), 3, dtype=torch.float64)
+    k = seeded((B, S, D), 4, dtype=torch.float64)
+    do = seeded((B, H, S, DV), 5, dtype=torch.float64)
+    o, m, l = R.dmla_fwd_cache_latent(q, k, DV, 0.4, True, torch.float64)
+    dq, dk = R.dmla_bwd_cache_latent(q, k, o, do, m, l, DV, 0.4, True, torch.float64)
+    dq2, dk2 = R.dmla_grads_autograd(q, k, do, DV, 0.4, True)
+    torch.testing.assert_close(dq, dq2, atol=1e-12, rtol=1e-10)
+    torch.testing.assert_close(dk, dk2, atol=1e-12, rtol=1e-10)
+
+    def f(qq, kk):
+        return R.dmla_fwd_cache_latent(qq, kk, DV, 0.4, True, torch.float64)[0]
+
+    assert torch.autograd.gradcheck(f, (q[:1, :1, :5].clone().requires_grad_(True),
+                                        k[:1, :5].clone().requires_grad_(True)))
+
+
+# ---------------------------------------------------------------- closed forms / invariants
+def test_causal_first_row_is_first_value():
+    q = seeded((1, 2, 9, 16), 6, dtype=torch.float64)
+    k = seeded((1, 9, 16), 7, dtype=torch.float64)
+    o, m, l = R.dmla_fwd_cache_latent(q, k, 8, 0.5, True, torch.float64)
+    torch.testing.assert_close(o[0, :, 0], k[0, 0, :8].expand(2, 8), atol=0, rtol=0)
+    torch.testing.assert_close(l[0, :, 0], torch.ones(2, dtype=torch.float64))
+
+
+def test_zero_query_gives_prefix_mean():
+    k = seeded((1, 10, 16), 8, dtype=torch.float64)
+    q = torch.zeros(1, 3, 10, 16, dtype=torch.float64)
+    o, _, l = R.dmla_fwd_cache_latent(q, k, 8, 0.5, True, torch.float64)
+    prefix_mean = torch.cumsum(k[0, :, :8], 0) / torch.arange(1, 11, dtype=torch.float64).unsqueeze(1)
+    torch.testing.assert_close(o[0, 1], prefix_mean, atol=1e-14, rtol=1e-14)
+    torch.testing.assert_close(l[0, 0], torch.arange(1, 11, dtype=torch.float64))
+
+
+def test_head_permutation_equivariance():
+    q = seeded((2, 5, 7, 16), 9, dtype=torch.float64)
+    k = seeded((2, 7, 16), 10, dtype=torch.float64)
+    perm = torch.tensor([3, 0, 4, 1, 2])
+    o, m, l = R.dmla_fwd_cache_latent(q, k, 8, 0.5, True, torch.float64)
+    o2, m2, l2 = R.dmla_fwd_cache_latent(q[:, perm], k, 8, 0.5, True, torch.float64)
+    torch.testing.assert_close(o2, o[:, perm], atol=0, rtol=0)
+    torch.testing.assert_close(l2, l[:, perm], atol=0, rtol=0)
+
+
+def test_fully_masked_rows_follow_the_guard():
+    # Sq > Sk with bottom-right alignment leaves the first Sq - Sk rows without keys.
+    q = seeded((1, 1, 6, 8), 11, dtype=torch.float64)
+    k = seeded((1, 4, 8), 12, dtype=torch.float64)
+    o, m, l = R.dmla_fwd_cache_latent(q, k, 4, 0.5, True, torch.float64)
+    assert torch.all(o[0, 0, :2] == 0) and torch.all(l[0, 0, :2] == 0)
+    assert torch.all(torch.isinf(m[0, 0, :2])) and torch.all(m[0, 0, :2] < 0)
+    assert torch.all(l[0, 0, 2:] > 0)
+
+
+@pytest.mark.parametrize("block", [1, 5, 16, 64])
+def test_online_recurrence_equals_exact(block):
+    q = seeded((2, 3, 33, 16), 13, dtype=torch.float64)
+    k = seeded((2, 1, 33, 16), 14, dtype=torch.float64)
+    v = k[..., :8]
+    o, m, l = R.attention_exact(q, k, v, 0.7, True)
+    o2, m2, l2 = R.attention_online(q, k, v, 0.7, True, block)
+    torch.testing.assert_close(o2, o, atol=1e-13, rtol=1e-12)
+    torch.testing.assert_close(m2, m, atol=0, rtol=0)
+    torch.testing.assert_close(l2, l, atol=1e-12, rtol=1e-12)
+
+
+def test_onthefly_is_cache_latent_per_head():
+    B, H, S, DIN, DL = 2, 3, 13, 10, 6
+    q = seeded((B, H, S, DL), 15, dtype=torch.float64)
+    k = seeded((B, S, H, DIN), 16, dtype=torch.float64)
+    v = seeded((B, S, H, DIN), 17, dtype=torch.float64)
+    wk = seeded((H, DIN, DL), 18, dtype=torch.float64)
+    wv = seeded((H, DIN, DL), 19, dtype=torch.float64)
+    o, m, l = R.dmla_fwd_onthefly(q, k, v, wk, wv, 0.4, True, torch.float64)
+    for h in range(H):
+        kl = k[:, :, h] @ wk[h]
+        vl = v[:, :, h] @ wv[h]
+        ref = F.scaled_dot_product_attention(q[:, h], kl, vl, is_causal=True, scale=0.4)
+        torch.testing.assert_close(o[:, h], ref, atol=1e-12, rtol=1e-12)
+
+
+def test_decode_paged_equals_contiguous_and_ignores_page_order():
+    B, H, D, DV, P = 3, 4, 16, 8, 4
+    lens = torch.tensor([1, 9, 14], dtype=torch.int32)
+    n_pages = [(int(n) + P - 1) // P for n in lens]
+    total = sum(n_pages)
+    seqs = [seeded((int(n), D), 20 + i, dtype=torch.float64) for i, n in enumerate(lens)]
+    q = seeded((B, H, D), 30, dtype=torch.float64)
+    for perm_seed in (0, 1):
+        perm = torch.randperm(total, generator=torch.Generator().manual_seed(perm_seed))
+        pool = torch.full((total, P, D), float("nan"), dtype=torch.float64)  # unused rows are NaN
+        table = torch.zeros(B, 4, dtype=torch.int32)
+        c = 0
+        for b in range(B):
+            for j in range(n_pages[b]):
+                page = int(perm[c]); c += 1
+                table[b, j] = page
+                rows = seqs[b][j * P:(j + 1) * P]
+                pool[page, :rows.shape[0]] = rows
+        o, lse = R.dmla_decode_paged(q, pool, table, lens, DV, 0.5, torch.float64)
+        for b in range(B):
+            ref, m, l = R.attention_exact(q[b].unsqueeze(1), seqs[b].unsqueeze(0), seqs[b][:, :DV].unsqueeze(0), 0.5, False)
+            torch.testing.assert_close(o[b], ref.squeeze(1), atol=1e-14, rtol=1e-13)
+            torch.testing.assert_close(lse[b], (m + torch.log(l)).squeeze(1), atol=1e-13, rtol=1e-13)
+
+
+# ---------------------------------------------------------------- planted mistakes
+def _mutant_bwd(q, k, o, do, m, l, d_v, scale, mistake):
+    s = R.masked_scores(q[0], k[0].unsqueeze(0), scale, True)
+    p = torch.exp(s - m[0].unsqueeze(-1)) / l[0].unsqueeze(-1)
+    v = k[0, :, :d_v]
+    delta = (do[0] * o[0]).sum(-1)
+    dp = do[0] @ v.t()
+    ds = p * (dp - delta.unsqueeze(-1))
+    dq_scale = 1.0 if mistake == "dq_no_scale" else scale
+    dq = dq_scale * ds @ k[0]
+    dk = scale * (ds.transpose(-1, -2) @ q[0]).sum(0)
+    if mistake != "no_v_fold":
+        dk[:, :d_v] += (p.transpose(-1, -2) @ do[0]).sum(0)
+    return dq.unsqueeze(0), dk.unsqueeze(0)
+
+
+@pytest.mark.parametrize("mistake", ["dq_no_scale", "no_v_fold"])
+def test_planted_backward_mistakes_are_caught(mistake):
+    g = _golden()
+    q, k, do = (torch.from_numpy(g[n]).double() for n in ("q", "k_lat", "do"))
+    o, m, l = R.dmla_fwd_cache_latent(q, k, 32, 1 / 8, True, torch.float64)
+    dq, dk = _mutant_bwd(q, k, o, do, m, l, 32, 1 / 8, mistake)
+    bad = not (np.allclose(dq.numpy(), g["dq"], atol=1e-5) and np.allclose(dk.numpy(), g["dk_lat"], atol=1e-5))
+    assert bad, f"golden gradients failed to catch the planted mistake {mistake}"
+
+
+@pytest.mark.parametrize("mistake", ["v_wrong_slice", "k_transposed_dims", "unscaled_m"])
+def test_planted_forward_mistakes_are_caught(mistake):
+    g = _golden()
+    q, k = torch.from_numpy(g["q"]).double(), torch.from_numpy(g["k_lat"]).double()
+    if mistake == "v_wrong_slice":
+        o, m, l = R.attention_exact(q[0], k, k[..., -32:], 1 / 8, True)
+    elif mistake == "k_transposed_dims":
+        o, m, l = R.attention_exact(q[0], k.flip(-1), k[..., :32], 1 / 8, True)
+    else:
+        o, m, l = R.attention_exact(q[0], k, k[..., :32], 1 / 8, True)
+        m = m * 8.0
+    same = (np.allclose(o.numpy(), g["o"][0], atol=1e-5) and np.allclose(m.numpy(), g["m"][0], atol=1e-5))
+    assert not same, f"golden forward failed to catch the planted mistake {mistake}"
