@@ -10,11 +10,13 @@
 //    all heads of a position share one causal limit and the workgroup streams ONE latent key
 //    sequence: prefill is multi-query attention with M = 64 rows per key tile, decode puts 64
 //    heads of one sequence in M.
-//  * 4 waves, one per SIMD, arranged as 2 pairs.  A pair owns 32 rows; its two waves split the
-//    work in halves: wave half h holds Q[:, 288h .. 288h+287] (72 VGPRs) and accumulates
-//    O[:, 256h .. 256h+255] (128 fp32 AGPR/VGPRs).  Partial scores over each half of the 576
-//    dims are summed through LDS.  Every byte of K/V read from LDS feeds 32 rows, as in a
-//    32-rows-per-wave design, at ~300 instead of ~470 live registers per lane.
+//  * 4 waves, one per SIMD.  S^T = K . Q^T is computed by 2 pairs: a pair owns 32 rows and its
+//    waves split the 576 contraction dims in halves (Q half: 72 VGPRs); each wave posts the
+//    partial scores of its partner's 16 rows to LDS and finalises the softmax of its own 16.
+//    P of all 64 rows is then shared through LDS and every wave accumulates O for all 64 rows
+//    over its own 128 output columns (128 fp32 accumulators).  K operands (b128 reads) feed
+//    32 rows and V operands (ds_read_b64_tr_b16, the slow LDS path) feed all 64 rows, at ~300
+//    live registers per lane.
 //  * Key tiles of 32 rows x 576 (36 KB) are copied global -> LDS with 16-byte direct loads
 //    (no VGPR staging) into a 3-deep ring, two tiles ahead of use.
 //  * S^T = K_tile . Q^T on v_mfma_f32_16x16x32_bf16 leaves each lane holding one query's scores
@@ -41,11 +43,16 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kRowsPerWG = 64;
 constexpr int kKcHalf = kDqk / 32 / 2;              // 9 k-steps per dims half
-constexpr int kDbHalf = kDv / 16 / 2;               // 16 output column blocks per half
+constexpr int kDbWave = kDv / 16 / kWaves;          // 8 output column blocks (128 columns) per wave
 constexpr int kDmaPerWave = kTileBytes / 1024 / kWaves;  // 9 one-KB DMA instructions
-constexpr int kXBytes = kWaves * 4096;              // partial-score exchange, one buffer
+constexpr int kXBytes = kWaves * 2048;              // partial-score exchange, one buffer
+constexpr int kPBytes = 4 * 1024;                   // P of the 64 rows as MFMA B operands
 constexpr int kMaxSplitPages = 1024;                // page-table cache of one decode split
-constexpr int kLdsBytes = kRing * kTileBytes + 2 * kXBytes + kMaxSplitPages * 4;
+constexpr int kXOffset = kRing * kTileBytes;
+constexpr int kPOffset = kXOffset + 2 * kXBytes;
+constexpr int kStatOffset = kPOffset + kPBytes;
+constexpr int kPageOffset = kStatOffset + kRowsPerWG * 4;
+constexpr int kLdsBytes = kPageOffset + kMaxSplitPages * 4;
 constexpr float kHeadroom = 32.0f;                  // log2 headroom of p over the reference max
 constexpr int kPrefetch = 4;                        // operand loads kept ahead of the MFMAs
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
@@ -114,11 +121,14 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const Work& wk,
   const int g = lane >> 4;
   const int pair = wave >> 1;
   const int b = wk.b, row0 = wk.row0, tile_begin = wk.tile_begin, tile_end = wk.tile_end;
-  DMLA_LDS char* xbuf = lds + kRing * kTileBytes;
-  const DMLA_LDS int* page_cache = reinterpret_cast<const DMLA_LDS int*>(xbuf + 2 * kXBytes);
+  DMLA_LDS char* xbuf = lds + kXOffset;
+  DMLA_LDS char* pbuf = lds + kPOffset;
+  DMLA_LDS float* inv_l_lds = reinterpret_cast<DMLA_LDS float*>(lds + kStatOffset);
+  const DMLA_LDS int* page_cache = reinterpret_cast<const DMLA_LDS int*>(lds + kPageOffset);
 
   const int nrows = kDecode ? p.H : p.H * p.Sq;
-  auto row_of = [&](int qg) { return row0 + pair * 32 + qg * 16 + l16; };
+  // Workgroup row r (0..63) -> global row; this wave finalises the softmax of rows 16*wave..+15.
+  const int own_row = row0 + 16 * wave + l16;
   auto limit_of = [&](int r) -> int {
     if constexpr (!kDecode) {
       const int pos = r / p.H;
@@ -130,11 +140,13 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const Work& wk,
   // Tiles whose last key is <= the smallest limit in the workgroup need no mask.
   const int wg_min_lim = limit_of(row0);
 
-  // ---- Q half as MFMA B operand: lane holds Q[row 16qg+l16][288 half + 32c + 8g .. +7] ----
+  // ---- Q: the pair's 32 rows, this wave's dims half, as MFMA B operand --------------------
+  // lane holds Q[row 32 pair + 16 qg + l16][288 kHalf + 32 c + 8 g .. +7]
   bf16x8 qreg[2][kKcHalf];
 #pragma unroll
   for (int qg = 0; qg < 2; ++qg) {
-    const int r = row_of(qg) < nrows ? row_of(qg) : 0;
+    const int rq = row0 + 32 * pair + 16 * qg + l16;
+    const int r = rq < nrows ? rq : 0;
     const bf16* qrow;
     if constexpr (!kDecode) {
       const int pos = r / p.H, head = r - pos * p.H;
@@ -151,16 +163,17 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const Work& wk,
   wait_vmem();
 
   // ---- tile staging ----------------------------------------------------------------------
-  // DMA instruction i (0..35) fills LDS bytes [1024 i, 1024 i + 1024) of the slot = chunk group
-  // i/4, rows 8(i%4) .. +7.  Lane l covers row 8(i%4) + l/8 at physical chunk l%8, i.e.
-  // logical chunk (l%8) ^ swz(row & 15), which depends only on the lane and on bit 3 of row.
+  // Copy j (0..8) of wave w fills LDS bytes [1024 (4j + w), +1024) of the slot: chunk group j,
+  // rows 8w .. 8w+7.  Lane l covers row 8w + l/8 at physical chunk l%8, i.e. logical chunk
+  // (l%8) ^ swz(row): one per-lane offset serves all nine copies; the chunk group's 128-byte
+  // column offset goes into the scalar base (the copy's immediate offset would also move the
+  // LDS destination).
   bool bad_page = false;
   const int row_stride_bytes = (int)(p.k_ss * 2);
-  const int dma_lane_row = lane >> 3;
-  const unsigned dma_off0 = dma_lane_row * row_stride_bytes + 16 * ((lane & 7) ^ swz(dma_lane_row));
-  const unsigned dma_off8 = dma_lane_row * row_stride_bytes + 16 * ((lane & 7) ^ swz(dma_lane_row + 8));
-  const unsigned dma_row0_off = 16 * ((lane & 7) ^ swz(0));
-  const unsigned lds_base = lds_addr(lds);
+  const int dma_row = 8 * wave + (lane >> 3);
+  const unsigned dma_col = 16 * ((lane & 7) ^ swz(dma_row));
+  const unsigned dma_off = (unsigned)(dma_row * row_stride_bytes) + dma_col;
+  const unsigned lds_base = lds_addr(lds) + 1024 * wave;
   auto stage = [&](int tile) {
     const char* tile_base;
     int valid_rows;
@@ -175,27 +188,21 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const Work& wk,
                                                 (int64_t)(tile % (kPage / kTileN)) * kTileN * p.k_ss);
       valid_rows = wk.ctx - tile * kTileN;
     }
+    // Rows past the valid range re-read row 0 of the tile: finite data, masked later.
+    const unsigned off = dma_row < valid_rows ? dma_off : dma_col;
     const unsigned dst = lds_base + ((tile - tile_begin) % kRing) * kTileBytes;
-    if (valid_rows >= kTileN) {
-#pragma unroll
-      for (int j = 0; j < kDmaPerWave; ++j) {
-        const int i = j * kWaves + wave;
-        const int r0 = 8 * (i & 3), cg = i >> 2;
-        dma16(tile_base + (r0 * row_stride_bytes + cg * 128), (r0 & 8) ? dma_off8 : dma_off0, dst + i * 1024);
-      }
-    } else {
-      // Rows past the valid range re-read row 0 of the tile: finite data, masked later.
-#pragma unroll
-      for (int j = 0; j < kDmaPerWave; ++j) {
-        const int i = j * kWaves + wave;
-        const int r0 = 8 * (i & 3), cg = i >> 2;
-        const bool ok = r0 + dma_lane_row < valid_rows;
-        const unsigned off = ok ? (unsigned)(r0 * row_stride_bytes) + ((r0 & 8) ? dma_off8 : dma_off0) : dma_row0_off;
-        dma16(tile_base + cg * 128, off, dst + i * 1024);
-      }
-    }
+    dma16(tile_base + 0 * 128, off, dst + 0 * 4096);
+    dma16(tile_base + 1 * 128, off, dst + 1 * 4096);
+    dma16(tile_base + 2 * 128, off, dst + 2 * 4096);
+    dma16(tile_base + 3 * 128, off, dst + 3 * 4096);
+    dma16(tile_base + 4 * 128, off, dst + 4 * 4096);
+    dma16(tile_base + 5 * 128, off, dst + 5 * 4096);
+    dma16(tile_base + 6 * 128, off, dst + 6 * 4096);
+    dma16(tile_base + 7 * 128, off, dst + 7 * 4096);
+    dma16(tile_base + 8 * 128, off, dst + 8 * 4096);
   };
-  // Wait for this wave's DMA of the tile about to be used; the next tile's may stay in flight.
+  static_assert(kGroups == 9 && kDmaPerWave == 9, "staging is written out for 9 chunk groups");
+  // Wait for this wave's copy of the tile about to be used; the next tile's may stay in flight.
   auto wait_tile = [&](int t) {
     if (t + 1 < tile_end) __builtin_amdgcn_s_waitcnt(0x0f70 | kDmaPerWave);  // vmcnt(9)
     else wait_vmem();
@@ -208,93 +215,33 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const Work& wk,
   const int k_off[2] = {l16 * 128 + 16 * (g ^ ksw), l16 * 128 + 16 * ((4 + g) ^ ksw)};
   // V operand (A of O^T) through transpose reads: lane 4e+q of group g reads row 4g+e (and
   // 16+4g+e), columns 16db + 4q .. +3 = chunk group db/4, in-group chunk 2(db%4) + (q>>1),
-  // byte 8(q&1) inside the chunk.
+  // byte 8(q&1) inside the chunk.  This wave's output columns are 128 wave .. +127, i.e.
+  // db = 8 wave + d, chunk groups 2 wave + d/4.
   const int e = l16 >> 2, qq = l16 & 3;
   const int vsw = swz(4 * g + e);
   int v_off[4];
 #pragma unroll
-  for (int d = 0; d < 4; ++d) v_off[d] = (4 * g + e) * 128 + 16 * ((2 * d + (qq >> 1)) ^ vsw) + 8 * (qq & 1);
-  // Partial-score exchange slots: [buffer][wave][j = 2kb + qg][lane] x 16 B.
-  const int x_own = wave * 4096 + lane * 16;
-  const int x_peer = (wave ^ 1) * 4096 + lane * 16;
+  for (int d = 0; d < 4; ++d)
+    v_off[d] = 2 * wave * kGroupBytes + (4 * g + e) * 128 + 16 * ((2 * d + (qq >> 1)) ^ vsw) + 8 * (qq & 1);
+  // Exchange slots (16 B per lane): partial scores [buffer][wave][kb][lane], P [qg][lane].
+  const int x_post = wave * 2048 + lane * 16;
+  const int x_take = (wave ^ 1) * 2048 + lane * 16;
+  const int p_post = wave * 1024 + lane * 16;
 
-  // Full scores S^T[key 16kb + 4g + i][query 16qg + l16] of tile t in the exp2 domain, masked.
-  auto scores = [&](int t, float (&x)[2][8]) {
-    const DMLA_LDS char* tb = lds + ((t - tile_begin) % kRing) * kTileBytes;
-    f32x4 sacc[2][2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      sacc[kb][0] = sacc[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < kKcHalf; ++c) {
-        constexpr int c0 = kHalf * kKcHalf;
-        const int cc = c0 + c;
-        const int off = k_off[cc & 1] + (cc >> 1) * kGroupBytes + kb * 16 * 128;
-        const bf16x8 a = lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(tb + off));
-        sacc[kb][0] = mfma_bf16(a, qreg[0][c], sacc[kb][0]);
-        sacc[kb][1] = mfma_bf16(a, qreg[1][c], sacc[kb][1]);
-      }
-    }
-    pipeline_schedule<2 * kKcHalf, 1, kPrefetch>();
-    // Sum the two dims halves through LDS.  Both waves add the same two partials (a+b == b+a),
-    // so the pair holds bitwise-identical scores and takes identical softmax decisions.
-    DMLA_LDS char* xb = xbuf + (t & 1) * kXBytes;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<DMLA_LDS f32x4*>(xb + x_own + j * 1024) = sacc[j >> 1][j & 1];
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      sacc[j >> 1][j & 1] += *reinterpret_cast<const DMLA_LDS f32x4*>(xb + x_peer + j * 1024);
-    const int key0 = t * kTileN;
-    const bool need_mask = key0 + kTileN - 1 > wg_min_lim;
-#pragma unroll
-    for (int qg = 0; qg < 2; ++qg) {
-      const int lim = need_mask ? limit_of(row_of(qg)) : 0;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float v = sacc[kb][qg][i] * p.scale_log2;
-          if (need_mask) v = key0 + 16 * kb + 4 * g + i > lim ? kNegInf : v;
-          x[qg][kb * 4 + i] = v;
-        }
-    }
-  };
+  f32x4 oacc[kDbWave][4];   // O^T[128 wave + 16 d + 4 g + i][16 qg + l16]
+  float mref;               // max the accumulators of the own rows are relative to
+  float mtrue;              // exact running max of this lane's keys of its own row
+  float lsum;               // this lane's partial row sum relative to mref
+  float mref_init = kNegInf;
 
-  f32x4 oacc[kDbHalf][2];
-  float mref[2];   // max the accumulators are relative to (fixed once set)
-  float mtrue[2];  // exact running max of this lane's keys
-  float lsum[2];   // this lane's partial row sum relative to mref
-
-  for (int pass = 0; pass < 2; ++pass) {
-    if (pass == 1) {
-      // Exact row max of the whole row tile, then recompute with mref fixed to it.
-      float mx[2] = {kNegInf, kNegInf};
-      if (tile_begin < tile_end) stage(tile_begin);
-      if (tile_begin + 1 < tile_end) stage(tile_begin + 1);
-      for (int t = tile_begin; t < tile_end; ++t) {
-        wait_tile(t);
-        __syncthreads();
-        if (t + 2 < tile_end) stage(t + 2);
-        float x[2][8];
-        scores(t, x);
+  for (;;) {
 #pragma unroll
-        for (int qg = 0; qg < 2; ++qg)
+    for (int d = 0; d < kDbWave; ++d)
 #pragma unroll
-          for (int j = 0; j < 8; ++j) mx[qg] = fmaxf(mx[qg], x[qg][j]);
-      }
-      wait_vmem();
-      __syncthreads();
-      mref[0] = group_max(mx[0]);
-      mref[1] = group_max(mx[1]);
-    } else {
-      mref[0] = mref[1] = kNegInf;
-    }
-#pragma unroll
-    for (int db = 0; db < kDbHalf; ++db) oacc[db][0] = oacc[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    mtrue[0] = mtrue[1] = kNegInf;
-    lsum[0] = lsum[1] = 0.f;
+      for (int qg = 0; qg < 4; ++qg) oacc[d][qg] = f32x4{0.f, 0.f, 0.f, 0.f};
+    mref = mref_init;
+    mtrue = kNegInf;
+    lsum = 0.f;
     int overflow = 0;
 
     if (tile_begin < tile_end) stage(tile_begin);
@@ -304,109 +251,147 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const Work& wk,
       if (__syncthreads_or(overflow)) break;
       if (t + 2 < tile_end) stage(t + 2);
       const DMLA_LDS char* tb = lds + ((t - tile_begin) % kRing) * kTileBytes;
-      float x[2][8];
-      scores(t, x);
-      float mloc[2];
-#pragma unroll
-      for (int qg = 0; qg < 2; ++qg) {
-        float mx = x[qg][0];
-#pragma unroll
-        for (int j = 1; j < 8; ++j) mx = fmaxf(mx, x[qg][j]);
-        mloc[qg] = mx;
-        mtrue[qg] = fmaxf(mtrue[qg], mx);
-      }
-      // A row seeing its first finite scores adopts the group max as mref (its O and l are
-      // still zero); a row whose scores climb past mref + kHeadroom requests pass 1.
-      const bool unset = (mref[0] == kNegInf && mloc[0] != kNegInf) || (mref[1] == kNegInf && mloc[1] != kNegInf);
-      if (__any(unset)) {
-#pragma unroll
-        for (int qg = 0; qg < 2; ++qg) {
-          const float mt = group_max(mloc[qg]);
-          if (mref[qg] == kNegInf) mref[qg] = mt;
-        }
-      }
-      if (mloc[0] > mref[0] + kHeadroom || mloc[1] > mref[1] + kHeadroom) overflow = 1;
-      bf16x8 pk[2];  // [qg]: keys {4g..4g+3, 16+4g..16+4g+3}
-#pragma unroll
-      for (int qg = 0; qg < 2; ++qg) {
-        const float ms = mref[qg] == kNegInf ? 0.f : mref[qg];
-        float ls = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float pv = fast_exp2(fminf(x[qg][j] - ms, kHeadroom));
-          ls += pv;
-          pk[qg][j] = (bf16)pv;
-        }
-        lsum[qg] += ls;
-      }
 
-      // O^T[dv][query] += V^T . P^T over this wave's half of the output columns.
+      // ---- partial S^T[key 16kb + 4g + i][pair row 16qg + l16] over this wave's dims half ----
+      f32x4 sacc[2][2];
 #pragma unroll
-      for (int d = 0; d < kDbHalf; ++d) {
-        constexpr int db0 = kHalf * kDbHalf;
-        const int db = db0 + d;
-        const int base = v_off[db & 3] + (db >> 2) * kGroupBytes;
+      for (int kb = 0; kb < 2; ++kb) {
+        sacc[kb][0] = sacc[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < kKcHalf; ++c) {
+          constexpr int c0 = kHalf * kKcHalf;
+          const int cc = c0 + c;
+          const int off = k_off[cc & 1] + (cc >> 1) * kGroupBytes + kb * 16 * 128;
+          const bf16x8 a = lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(tb + off));
+          sacc[kb][0] = mfma_bf16(a, qreg[0][c], sacc[kb][0]);
+          sacc[kb][1] = mfma_bf16(a, qreg[1][c], sacc[kb][1]);
+        }
+      }
+      pipeline_schedule<2 * kKcHalf, 1, kPrefetch>();
+      // Post the partner's rows, take ours: S of the own 16 rows summed over both dims halves.
+      DMLA_LDS char* xb = xbuf + (t & 1) * kXBytes;
+      *reinterpret_cast<DMLA_LDS f32x4*>(xb + x_post) = sacc[0][1 - kHalf];
+      *reinterpret_cast<DMLA_LDS f32x4*>(xb + x_post + 1024) = sacc[1][1 - kHalf];
+      __syncthreads();
+      const f32x4 s0 = sacc[0][kHalf] + *reinterpret_cast<const DMLA_LDS f32x4*>(xb + x_take);
+      const f32x4 s1 = sacc[1][kHalf] + *reinterpret_cast<const DMLA_LDS f32x4*>(xb + x_take + 1024);
+
+      // ---- online softmax of the own rows (exp2 domain) --------------------------------------
+      const int key0 = t * kTileN;
+      float x[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[i] = s0[i] * p.scale_log2;
+        x[4 + i] = s1[i] * p.scale_log2;
+      }
+      if (key0 + kTileN - 1 > wg_min_lim) {
+        const int lim = own_row < nrows ? limit_of(own_row) : -1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[i] = key0 + 4 * g + i > lim ? kNegInf : x[i];
+          x[4 + i] = key0 + 16 + 4 * g + i > lim ? kNegInf : x[4 + i];
+        }
+      }
+      float mloc = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+      mtrue = fmaxf(mtrue, mloc);
+      // A row seeing its first finite scores adopts their group max as mref (its O and l are
+      // still zero); a row whose scores climb past mref + kHeadroom requests a restart.
+      if (__any(mref == kNegInf && mloc != kNegInf)) {
+        const float mt = group_max(mloc);
+        if (mref == kNegInf) mref = mt;
+      }
+      if (mloc > mref + kHeadroom) overflow = 1;
+      const float ms = mref == kNegInf ? 0.f : mref;
+      bf16x8 pk;  // keys {4g..4g+3, 16+4g..16+4g+3} of the own row
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float pv = fast_exp2(x[j] - ms);
+        lsum += pv;
+        pk[j] = (bf16)pv;
+      }
+      *reinterpret_cast<DMLA_LDS bf16x8*>(pbuf + p_post) = pk;
+      __syncthreads();
+
+      // ---- O^T[dv][row] += V^T . P^T for this wave's 128 columns and all 64 rows -------------
+      bf16x8 pall[4];
+#pragma unroll
+      for (int qg = 0; qg < 4; ++qg) pall[qg] = *reinterpret_cast<const DMLA_LDS bf16x8*>(pbuf + qg * 1024 + lane * 16);
+#pragma unroll
+      for (int d = 0; d < kDbWave; ++d) {
+        const int base = v_off[d & 3] + (d >> 2) * kGroupBytes;
         const bf16x4 v0 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tb + base));
         const bf16x4 v1 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tb + base + 16 * 128));
         const bf16x8 a = concat(v0, v1);
-        oacc[d][0] = mfma_bf16(a, pk[0], oacc[d][0]);
-        oacc[d][1] = mfma_bf16(a, pk[1], oacc[d][1]);
+#pragma unroll
+        for (int qg = 0; qg < 4; ++qg) oacc[d][qg] = mfma_bf16(a, pall[qg], oacc[d][qg]);
       }
-      pipeline_schedule<kDbHalf, 2, kPrefetch>();
     }
     wait_vmem();
     if (!__syncthreads_or(overflow)) break;
+    // Restart with every row's reference max raised to the largest score seen so far: tiles up
+    // to the overflowing one cannot overflow again, so each restart gets strictly further.
+    mref_init = fmaxf(mref_init, group_max(mtrue));
   }
 
   // ---- epilogue ---------------------------------------------------------------------------
   const bool poison = kDecode && __any(bad_page);
   const float nanv = __builtin_nanf("");
+  const float ltot = group_sum(lsum);
+  const float mt = group_max(mtrue);
+  if (g == 0) inv_l_lds[16 * wave + l16] = ltot > 0.f ? 1.f / ltot : 0.f;
+  // Statistics of the own rows.
+  if (g == 0 && own_row < nrows) {
+    if constexpr (!kDecode) {
+      if (p.m != nullptr) {
+        const int pos = own_row / p.H, head = own_row - pos * p.H;
+        const int si = (b * p.H + head) * p.Sq + pos;
+        p.m[si] = mt == kNegInf ? kNegInf : mt * kLn2;
+        p.l[si] = mt == kNegInf ? 0.f : ltot * fast_exp2(mref - mt);
+      }
+    } else {
+      const float lse = poison ? nanv : (ltot > 0.f ? (mref + __log2f(ltot)) * kLn2 : kNegInf);
+      if (wk.nsplit == 1) {
+        if (p.lse != nullptr) p.lse[b * p.H + own_row] = lse;
+      } else {
+        p.part_lse[((int64_t)b * p.max_splits + wk.split) * p.H + own_row] = lse;
+      }
+    }
+  }
+  __syncthreads();
+  const int col = 128 * wave + 4 * g;
 #pragma unroll
-  for (int qg = 0; qg < 2; ++qg) {
-    const int r = row_of(qg);
-    const float ltot = group_sum(lsum[qg]);
-    const float mt = group_max(mtrue[qg]);
-    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+  for (int qg = 0; qg < 4; ++qg) {
+    const int r = row0 + 16 * qg + l16;
     if (r >= nrows) continue;
-    const int col = kHalf * (kDv / 2) + 4 * g;
+    const float inv = inv_l_lds[16 * qg + l16];
     if constexpr (!kDecode) {
       const int pos = r / p.H, head = r - pos * p.H;
       bf16* orp = p.o + b * p.o_sb + head * p.o_sh + pos * p.o_ss + col;
 #pragma unroll
-      for (int d = 0; d < kDbHalf; ++d) {
+      for (int d = 0; d < kDbWave; ++d) {
         const f32x4 v = oacc[d][qg] * inv;
         bf16x4 w;
         w[0] = (bf16)v[0]; w[1] = (bf16)v[1]; w[2] = (bf16)v[2]; w[3] = (bf16)v[3];
         *reinterpret_cast<bf16x4*>(orp + 16 * d) = w;
       }
-      if (kHalf == 0 && g == 0 && p.m != nullptr) {
-        const int si = (b * p.H + head) * p.Sq + pos;
-        p.m[si] = mt == kNegInf ? kNegInf : mt * kLn2;
-        p.l[si] = mt == kNegInf ? 0.f : ltot * fast_exp2(mref[qg] - mt);
+    } else if (wk.nsplit == 1) {
+      bf16* orp = p.o + b * p.o_sb + r * p.o_sh + col;
+#pragma unroll
+      for (int d = 0; d < kDbWave; ++d) {
+        f32x4 v = oacc[d][qg] * inv;
+        if (poison) v = f32x4{nanv, nanv, nanv, nanv};
+        bf16x4 w;
+        w[0] = (bf16)v[0]; w[1] = (bf16)v[1]; w[2] = (bf16)v[2]; w[3] = (bf16)v[3];
+        *reinterpret_cast<bf16x4*>(orp + 16 * d) = w;
       }
     } else {
-      const float lse = poison ? nanv : (ltot > 0.f ? (mref[qg] + __log2f(ltot)) * kLn2 : kNegInf);
-      if (wk.nsplit == 1) {
-        bf16* orp = p.o + b * p.o_sb + r * p.o_sh + col;
+      const int64_t slot = ((int64_t)b * p.max_splits + wk.split) * p.H + r;
+      float* pp = p.part_o + slot * kDv + col;
 #pragma unroll
-        for (int d = 0; d < kDbHalf; ++d) {
-          f32x4 v = oacc[d][qg] * inv;
-          if (poison) v = f32x4{nanv, nanv, nanv, nanv};
-          bf16x4 w;
-          w[0] = (bf16)v[0]; w[1] = (bf16)v[1]; w[2] = (bf16)v[2]; w[3] = (bf16)v[3];
-          *reinterpret_cast<bf16x4*>(orp + 16 * d) = w;
-        }
-        if (kHalf == 0 && g == 0 && p.lse != nullptr) p.lse[b * p.H + r] = lse;
-      } else {
-        const int64_t slot = ((int64_t)b * p.max_splits + wk.split) * p.H + r;
-        float* pp = p.part_o + slot * kDv + col;
-#pragma unroll
-        for (int d = 0; d < kDbHalf; ++d) {
-          f32x4 v = oacc[d][qg] * inv;
-          if (poison) v = f32x4{nanv, nanv, nanv, nanv};
-          *reinterpret_cast<f32x4*>(pp + 16 * d) = v;
-        }
-        if (kHalf == 0 && g == 0) p.part_lse[slot] = lse;
+      for (int d = 0; d < kDbWave; ++d) {
+        f32x4 v = oacc[d][qg] * inv;
+        if (poison) v = f32x4{nanv, nanv, nanv, nanv};
+        *reinterpret_cast<f32x4*>(pp + 16 * d) = v;
       }
     }
   }
@@ -453,7 +438,7 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
     wk.tile_begin = wk.page_begin * (kPage / kTileN);
     wk.tile_end = min((wk.ctx + kTileN - 1) / kTileN, page_end * (kPage / kTileN));
     // Cache this split's page indices in LDS (read by the wave-uniform staging code).
-    DMLA_LDS int* page_cache = reinterpret_cast<DMLA_LDS int*>(lds + kRing * kTileBytes + 2 * kXBytes);
+    DMLA_LDS int* page_cache = reinterpret_cast<DMLA_LDS int*>(lds + kPageOffset);
     for (int i = threadIdx.x; i < page_end - wk.page_begin; i += kThreads)
       page_cache[i] = p.block_table[wk.b * p.bt_sb + wk.page_begin + i];
     __syncthreads();
