@@ -18,6 +18,7 @@ typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 #define DMLA_LDS __attribute__((address_space(3)))
 
@@ -44,9 +45,15 @@ __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirs
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved: the clobber only documents it
 __device__ __forceinline__ void dma16(const void* sbase, unsigned voff, unsigned lds_addr) {
+  // Both scalar operands are wave-uniform by construction; readfirstlane makes that explicit
+  // to the compiler (a no-op for values it already holds in SGPRs).
+  const uint64_t base = reinterpret_cast<uint64_t>(sbase);
+  const uint64_t sb = ((uint64_t)__builtin_amdgcn_readfirstlane((unsigned)(base >> 32)) << 32) |
+                      (unsigned)__builtin_amdgcn_readfirstlane((unsigned)base);
+  const unsigned sl = __builtin_amdgcn_readfirstlane(lds_addr);
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
-               : "s"(lds_addr), "v"(voff), "s"(sbase)
+               : "s"(sl), "v"(voff), "s"(reinterpret_cast<const void*>(sb))
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -65,18 +72,21 @@ __device__ __forceinline__ bf16x8 concat(const bf16x4& a, const bf16x4& b) {
   return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-// Cross-lane butterflies among the four 16-lane groups of a wave (the groups that share one
-// MFMA column): lanes l, l^16, l^32, l^48.
-__device__ __forceinline__ float xor_lanes(float v, int mask) {
-  return __shfl_xor(v, mask, 64);
-}
+// Reductions over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48: the lanes that
+// share one MFMA column) with the gfx950 row-swap instructions.  Called with the same value in
+// both operands, permlane16_swap / permlane32_swap return, in some order, a lane's value and
+// its partner's (l^16 / l^32); a symmetric combine of the pair therefore needs no lane select.
 __device__ __forceinline__ float group_max(float v) {
-  v = fmaxf(v, xor_lanes(v, 16));
-  return fmaxf(v, xor_lanes(v, 32));
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float group_sum(float v) {
-  v += xor_lanes(v, 16);
-  return v + xor_lanes(v, 32);
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // Wait until every outstanding vector-memory op of this wave (including LDS DMA) has landed.

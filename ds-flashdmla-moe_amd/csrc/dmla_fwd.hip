@@ -10,21 +10,23 @@
 //    all heads of a position share one causal limit and the workgroup streams ONE latent key
 //    sequence: prefill is multi-query attention with M = 64 rows per key tile, decode puts 64
 //    heads of one sequence in M.
-//  * 4 waves, one per SIMD.  S^T = K . Q^T is computed by 2 pairs: a pair owns 32 rows and its
-//    waves split the 576 contraction dims in halves (Q half: 72 VGPRs); each wave posts the
-//    partial scores of its partner's 16 rows to LDS and finalises the softmax of its own 16.
-//    P of all 64 rows is then shared through LDS and every wave accumulates O for all 64 rows
-//    over its own 128 output columns (128 fp32 accumulators).  K operands (b128 reads) feed
-//    32 rows and V operands (ds_read_b64_tr_b16, the slow LDS path) feed all 64 rows, at ~300
-//    live registers per lane.
 //  * Key tiles of 32 rows x 576 (36 KB) are copied global -> LDS with 16-byte direct loads
-//    (no VGPR staging) into a 3-deep ring, two tiles ahead of use.
-//  * S^T = K_tile . Q^T on v_mfma_f32_16x16x32_bf16 leaves each lane holding one query's scores
-//    for keys {4g..4g+3, 16+4g..16+4g+3}: exactly the B-operand layout PV needs.  PV
-//    (O^T += V^T P^T) reads V^T with ds_read_b64_tr_b16 from the same row-major tile.
-//  * Softmax in the exp2 domain against a reference max fixed at the first finite tile: p stays
-//    below 2^kHeadroom, so O is never rescaled inside the loop.  Scores climbing past that
-//    headroom trigger a recomputation of the row tile against its exact row max.
+//    (no VGPR staging) into a 3-slot ring.
+//  * 8 waves, two per SIMD.  Wave w = 4p + 2h + k computes partial scores
+//    S^T = K . Q^T for rows 32p..32p+31 (its pair), keys 16k..16k+15 (its key half) over dims
+//    288h..288h+287 (its dims half; Q half in 72 VGPRs), on v_mfma_f32_16x16x32_bf16 whose
+//    output leaves each lane one row's scores for 4 keys -- the B-operand layout PV needs.
+//    The partner wave w^2 holds the other dims half; the two swap halves through LDS and each
+//    finalises the softmax of 16 rows x 16 keys.  P of all 64 rows is shared through LDS and
+//    wave w accumulates O for all 64 rows over output columns 64w..64w+63 (64 fp32 VGPRs),
+//    reading V^T with ds_read_b64_tr_b16 (the slow LDS path, ~62 B/clk/CU on MI355X) once per
+//    workgroup.  ~210 live registers per lane, so two waves share each SIMD.
+//  * Software pipeline with one barrier per tile: iteration t runs PV(t-1) and the partial
+//    scores of tile t+1 on the matrix cores with softmax(t) in between, and each wave refills
+//    the chunk group it alone reads in PV (plus a rope slice) of the ring slot it just drained.
+//  * Softmax in the exp2 domain against a per-row reference max fixed at the first tile: p
+//    stays below 2^kHeadroom, so O is never rescaled.  Scores climbing past that headroom
+//    trigger a recomputation of the row tile from a higher reference.
 #include "dmla_common.h"
 #include "dmla_host.h"
 
@@ -38,25 +40,25 @@ constexpr int kTileN = 32;                          // keys per LDS tile
 constexpr int kGroups = kDqk / 64;                  // 9 chunk groups of 64 columns (128 B)
 constexpr int kGroupBytes = kTileN * 128;           // 4 KB: one chunk group of all tile rows
 constexpr int kTileBytes = kGroups * kGroupBytes;   // 36 KB
-constexpr int kRing = 3;                            // tiles in flight
-constexpr int kWaves = 4;
+constexpr int kRing = 3;                            // ring slots
+constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kRowsPerWG = 64;
 constexpr int kKcHalf = kDqk / 32 / 2;              // 9 k-steps per dims half
-constexpr int kDbWave = kDv / 16 / kWaves;          // 8 output column blocks (128 columns) per wave
-constexpr int kDmaPerWave = kTileBytes / 1024 / kWaves;  // 9 one-KB DMA instructions
-constexpr int kXBytes = kWaves * 2048;              // partial-score exchange, one buffer
+constexpr int kDbWave = kDv / 16 / kWaves;          // 4 output column blocks (64 columns) per wave
+constexpr int kXBytes = kWaves * 1024;              // partial-score exchange, one buffer
 constexpr int kPBytes = 4 * 1024;                   // P of the 64 rows as MFMA B operands
 constexpr int kMaxSplitPages = 1024;                // page-table cache of one decode split
 constexpr int kXOffset = kRing * kTileBytes;
 constexpr int kPOffset = kXOffset + 2 * kXBytes;
-constexpr int kStatOffset = kPOffset + kPBytes;
-constexpr int kPageOffset = kStatOffset + kRowsPerWG * 4;
+constexpr int kRowOffset = kPOffset + 2 * kPBytes;  // per-row exchange [3][2 key halves][64]
+constexpr int kFlagOffset = kRowOffset + 3 * 2 * kRowsPerWG * 4;
+constexpr int kPageOffset = kFlagOffset + kWaves * 4;
 constexpr int kLdsBytes = kPageOffset + kMaxSplitPages * 4;
 constexpr float kHeadroom = 32.0f;                  // log2 headroom of p over the reference max
-constexpr int kPrefetch = 4;                        // operand loads kept ahead of the MFMAs
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 static_assert(kPage % kTileN == 0, "a page holds whole tiles");
+static_assert(kGroups == kWaves + 1, "each wave copies its PV chunk group; the rope group is shared");
 
 // LDS tile layout: [chunk group cg (9)][row (32)][8 sixteen-byte chunks], 128 B per row slice,
 // so rows 2k and 2k+1 fall in opposite halves of the 64 x 4-byte banks.  The chunk at logical
@@ -67,19 +69,18 @@ static_assert(kPage % kTileN == 0, "a page holds whole tiles");
 // of rows r..r+7 (ds_read_b64_tr_b16 V operand).
 __host__ __device__ constexpr int swz(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
 
-// Scheduling template for an unrolled region of `steps` steps, each made of `reads` LDS reads
-// feeding 2 MFMAs: `prefetch` steps of reads first, then (2 MFMA, reads) pairs, then the
-// remaining MFMAs.  Keeps the scheduler from hoisting every read (and its registers) to the top.
-template <int steps, int reads, int prefetch>
-__device__ __forceinline__ void pipeline_schedule() {
-  __builtin_amdgcn_sched_group_barrier(0x100, reads * prefetch, 0);
+// Scheduling template of one pipelined tile iteration: 22 LDS operand reads (partials, P, V,
+// K) feeding 34 MFMAs, with vector ALU work slotted between them.  A few reads run ahead; the
+// rest are interleaved so in-flight operands stay within the register budget.
+__device__ __forceinline__ void iteration_schedule() {
+  __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
 #pragma unroll
-  for (int i = 0; i < steps - prefetch; ++i) {
+  for (int i = 0; i < 16; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, reads, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
   }
-#pragma unroll
-  for (int i = 0; i < prefetch; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
 }
 
 struct MqaParams {
@@ -115,20 +116,29 @@ struct Work {
 };
 
 template <bool kDecode, int kHalf>
-__device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const Work& wk, DMLA_LDS char* lds,
-                                             const int wave, const int lane) {
+__device__ __noinline__ void mqa_fwd_exact(const MqaParams* params, Work wk, DMLA_LDS char* lds, int wave, int lane);
+
+// kExact = false: the fast path, reference max = the row max of the first tile; on overflow it
+// hands the whole row tile to the kExact = true path, which first computes every row's exact
+// max in a scores-only pass and then runs the same pipeline against it.  The fast path never
+// contains the (register-hungry) retry code.
+template <bool kDecode, int kHalf, bool kExact>
+__device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams* params, const Work& wk,
+                                             DMLA_LDS char* lds, const int wave, const int lane) {
   const int l16 = lane & 15;
   const int g = lane >> 4;
-  const int pair = wave >> 1;
+  const int pair = wave >> 2;          // rows 32 pair .. +31 for the partial scores
+  const int kh = wave & 1;             // key half of the tile: keys 16 kh .. +15
+  const int rb = wave >> 1;            // own softmax rows 16 rb .. +15 (= 2 pair + kHalf)
   const int b = wk.b, row0 = wk.row0, tile_begin = wk.tile_begin, tile_end = wk.tile_end;
   DMLA_LDS char* xbuf = lds + kXOffset;
   DMLA_LDS char* pbuf = lds + kPOffset;
-  DMLA_LDS float* inv_l_lds = reinterpret_cast<DMLA_LDS float*>(lds + kStatOffset);
+  DMLA_LDS float* rowx = reinterpret_cast<DMLA_LDS float*>(lds + kRowOffset);
+  DMLA_LDS int* flags = reinterpret_cast<DMLA_LDS int*>(lds + kFlagOffset);
   const DMLA_LDS int* page_cache = reinterpret_cast<const DMLA_LDS int*>(lds + kPageOffset);
 
   const int nrows = kDecode ? p.H : p.H * p.Sq;
-  // Workgroup row r (0..63) -> global row; this wave finalises the softmax of rows 16*wave..+15.
-  const int own_row = row0 + 16 * wave + l16;
+  const int own_row = row0 + 16 * rb + l16;
   auto limit_of = [&](int r) -> int {
     if constexpr (!kDecode) {
       const int pos = r / p.H;
@@ -137,8 +147,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const Work& wk,
       return wk.ctx - 1;
     }
   };
-  // Tiles whose last key is <= the smallest limit in the workgroup need no mask.
-  const int wg_min_lim = limit_of(row0);
+  const int own_lim = own_row < nrows ? limit_of(own_row) : -1;
 
   // ---- Q: the pair's 32 rows, this wave's dims half, as MFMA B operand --------------------
   // lane holds Q[row 32 pair + 16 qg + l16][288 kHalf + 32 c + 8 g .. +7]
@@ -163,184 +172,256 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const Work& wk,
   wait_vmem();
 
   // ---- tile staging ----------------------------------------------------------------------
-  // Copy j (0..8) of wave w fills LDS bytes [1024 (4j + w), +1024) of the slot: chunk group j,
-  // rows 8w .. 8w+7.  Lane l covers row 8w + l/8 at physical chunk l%8, i.e. logical chunk
-  // (l%8) ^ swz(row): one per-lane offset serves all nine copies; the chunk group's 128-byte
-  // column offset goes into the scalar base (the copy's immediate offset would also move the
-  // LDS destination).
+  // Wave w copies chunk group w -- the output columns it alone reads in PV -- in 4 copies of 8
+  // rows, and waves 0..3 also copy rows 8w..8w+7 of the rope group 8, which only QK reads.
+  // A ring slot can therefore be refilled by each wave as soon as its own PV reads of it are
+  // done, without a barrier.  Lane l covers row 8r + l/8 at physical chunk l%8, i.e. logical
+  // chunk (l%8) ^ swz(row); the group's 128-byte column offset goes into the scalar base (an
+  // instruction offset would also move the LDS address).
   bool bad_page = false;
   const int row_stride_bytes = (int)(p.k_ss * 2);
-  const int dma_row = 8 * wave + (lane >> 3);
-  const unsigned dma_col = 16 * ((lane & 7) ^ swz(dma_row));
-  const unsigned dma_off = (unsigned)(dma_row * row_stride_bytes) + dma_col;
-  const unsigned lds_base = lds_addr(lds) + 1024 * wave;
-  auto stage = [&](int tile) {
-    const char* tile_base;
-    int valid_rows;
+  // Row 8r + l/8 of a copy has swizzle swz(8 (r & 1) + l/8): two column variants per lane.
+  const int dma_lrow = lane >> 3;
+  const unsigned dma_col[2] = {16u * ((lane & 7) ^ swz(dma_lrow)), 16u * ((lane & 7) ^ swz(8 + dma_lrow))};
+  const unsigned dma_lane = (unsigned)(dma_lrow * row_stride_bytes);
+  const int dma_rope_r = wave & 3;   // rope copy of waves 0..3: rows 8w .. 8w+7
+  const int ncopies = wave < 4 ? 5 : 4;
+  const unsigned lds_base = lds_addr(lds);
+  // Scalar base of tile `tile` (clamped into the work item, so copies past the end re-read the
+  // last tile: finite data in a slot nobody reads) and its count of valid rows.
+  auto tile_src = [&](int tile, int& valid_rows) -> const char* {
+    tile = min(tile, tile_end - 1);
     if constexpr (!kDecode) {
-      tile_base = reinterpret_cast<const char*>(p.kv + b * p.k_sb + (int64_t)tile * kTileN * p.k_ss);
       valid_rows = p.Sk - tile * kTileN;
+      return reinterpret_cast<const char*>(p.kv + b * p.k_sb + (int64_t)tile * kTileN * p.k_ss);
     } else {
       const int pg = tile / (kPage / kTileN);
       int page = uniform(page_cache[pg - wk.page_begin]);
       if (page < 0 || page >= p.num_pages) { bad_page = true; page = 0; }
-      tile_base = reinterpret_cast<const char*>(p.kv + (int64_t)page * p.k_sb +
-                                                (int64_t)(tile % (kPage / kTileN)) * kTileN * p.k_ss);
       valid_rows = wk.ctx - tile * kTileN;
+      return reinterpret_cast<const char*>(p.kv + (int64_t)page * p.k_sb +
+                                           (int64_t)(tile % (kPage / kTileN)) * kTileN * p.k_ss);
     }
-    // Rows past the valid range re-read row 0 of the tile: finite data, masked later.
-    const unsigned off = dma_row < valid_rows ? dma_off : dma_col;
-    const unsigned dst = lds_base + ((tile - tile_begin) % kRing) * kTileBytes;
-    dma16(tile_base + 0 * 128, off, dst + 0 * 4096);
-    dma16(tile_base + 1 * 128, off, dst + 1 * 4096);
-    dma16(tile_base + 2 * 128, off, dst + 2 * 4096);
-    dma16(tile_base + 3 * 128, off, dst + 3 * 4096);
-    dma16(tile_base + 4 * 128, off, dst + 4 * 4096);
-    dma16(tile_base + 5 * 128, off, dst + 5 * 4096);
-    dma16(tile_base + 6 * 128, off, dst + 6 * 4096);
-    dma16(tile_base + 7 * 128, off, dst + 7 * 4096);
-    dma16(tile_base + 8 * 128, off, dst + 8 * 4096);
   };
-  static_assert(kGroups == 9 && kDmaPerWave == 9, "staging is written out for 9 chunk groups");
-  // Wait for this wave's copy of the tile about to be used; the next tile's may stay in flight.
-  auto wait_tile = [&](int t) {
-    if (t + 1 < tile_end) __builtin_amdgcn_s_waitcnt(0x0f70 | kDmaPerWave);  // vmcnt(9)
-    else wait_vmem();
+  auto slot_addr = [&](int tile) { return lds_base + ((tile - tile_begin + kRing) % kRing) * kTileBytes; };
+  // Copy k (0..ncopies-1) of this wave; rows past the valid range re-read row 0 of the tile
+  // (finite data, masked later).
+  auto copy_part = [&](int k, const char* src, int valid_rows, unsigned dst) {
+    const int r = k < 4 ? k : dma_rope_r;
+    const unsigned col = (r & 1) ? dma_col[1] : dma_col[0];
+    const unsigned off = 8 * r + dma_lrow < valid_rows ? dma_lane + (unsigned)(8 * r * row_stride_bytes) + col : col;
+    if (k < 4) dma16(src + wave * 128, off, dst + wave * kGroupBytes + k * 1024);
+    else dma16(src + 8 * 128, off, dst + 8 * kGroupBytes + dma_rope_r * 1024);
+  };
+  auto stage = [&](int tile, int slot_tile) {
+    int valid_rows;
+    const char* src = tile_src(tile, valid_rows);
+    const unsigned dst = slot_addr(slot_tile);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) copy_part(k, src, valid_rows, dst);
+    if (ncopies > 4) copy_part(4, src, valid_rows, dst);
   };
 
   // ---- per-lane LDS byte offsets -----------------------------------------------------------
-  // K operand (A of S^T) for global k-step c: row 16kb + l16, logical chunk 4c + g = chunk
+  // K operand (A of S^T) for global k-step c: row 16 kh + l16, logical chunk 4c + g = chunk
   // group c/2, in-group position 4(c&1) + g.
   const int ksw = swz(l16);
-  const int k_off[2] = {l16 * 128 + 16 * (g ^ ksw), l16 * 128 + 16 * ((4 + g) ^ ksw)};
+  const int kh_off = kh * 16 * 128;
+  const int k_off[2] = {kh_off + l16 * 128 + 16 * (g ^ ksw), kh_off + l16 * 128 + 16 * ((4 + g) ^ ksw)};
   // V operand (A of O^T) through transpose reads: lane 4e+q of group g reads row 4g+e (and
   // 16+4g+e), columns 16db + 4q .. +3 = chunk group db/4, in-group chunk 2(db%4) + (q>>1),
-  // byte 8(q&1) inside the chunk.  This wave's output columns are 128 wave .. +127, i.e.
-  // db = 8 wave + d, chunk groups 2 wave + d/4.
+  // byte 8(q&1) inside the chunk.  This wave's output columns 64w.. are chunk group w.
   const int e = l16 >> 2, qq = l16 & 3;
   const int vsw = swz(4 * g + e);
-  int v_off[4];
+  int v_off[kDbWave];
 #pragma unroll
-  for (int d = 0; d < 4; ++d)
-    v_off[d] = 2 * wave * kGroupBytes + (4 * g + e) * 128 + 16 * ((2 * d + (qq >> 1)) ^ vsw) + 8 * (qq & 1);
-  // Exchange slots (16 B per lane): partial scores [buffer][wave][kb][lane], P [qg][lane].
-  const int x_post = wave * 2048 + lane * 16;
-  const int x_take = (wave ^ 1) * 2048 + lane * 16;
-  const int p_post = wave * 1024 + lane * 16;
+  for (int d = 0; d < kDbWave; ++d)
+    v_off[d] = wave * kGroupBytes + (4 * g + e) * 128 + 16 * ((2 * d + (qq >> 1)) ^ vsw) + 8 * (qq & 1);
+  // Exchange slots: partial scores [buffer][wave][lane] x 16 B; P [buffer][row block][lane] x
+  // 16 B with the key-half owner writing bytes 8 kh .. 8 kh + 7.
+  const int x_post = wave * 1024 + lane * 16;
+  const int x_take = (wave ^ 2) * 1024 + lane * 16;
+  const int p_post = rb * 1024 + lane * 16 + kh * 8;
 
-  f32x4 oacc[kDbWave][4];   // O^T[128 wave + 16 d + 4 g + i][16 qg + l16]
+  auto slot_of = [&](int t) { return lds + ((t - tile_begin + kRing) % kRing) * kTileBytes; };
+
+  f32x4 oacc[kDbWave][4];   // O^T[64 wave + 16 d + 4 g + i][16 qg + l16]
   float mref;               // max the accumulators of the own rows are relative to
   float mtrue;              // exact running max of this lane's keys of its own row
   float lsum;               // this lane's partial row sum relative to mref
   float mref_init = kNegInf;
+  const float scale_log2 = p.scale_log2;
 
-  for (;;) {
+  // PV of tile tp for this wave's 64 columns and all 64 rows.
+  auto pv = [&](int tp) {
+    const DMLA_LDS char* tb = slot_of(tp);
+    const DMLA_LDS char* pb = pbuf + (tp & 1) * kPBytes;
+    bf16x8 pall[4];
 #pragma unroll
-    for (int d = 0; d < kDbWave; ++d)
+    for (int qg = 0; qg < 4; ++qg) pall[qg] = *reinterpret_cast<const DMLA_LDS bf16x8*>(pb + qg * 1024 + lane * 16);
 #pragma unroll
-      for (int qg = 0; qg < 4; ++qg) oacc[d][qg] = f32x4{0.f, 0.f, 0.f, 0.f};
-    mref = mref_init;
-    mtrue = kNegInf;
-    lsum = 0.f;
-    int overflow = 0;
+    for (int d = 0; d < kDbWave; ++d) {
+      const bf16x4 v0 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tb + v_off[d]));
+      const bf16x4 v1 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tb + v_off[d] + 16 * 128));
+      const bf16x8 a = concat(v0, v1);
+#pragma unroll
+      for (int qg = 0; qg < 4; ++qg) oacc[d][qg] = mfma_bf16(a, pall[qg], oacc[d][qg]);
+    }
+  };
+  // Partial S^T[key 16 kh + 4g + i][pair row 16 qg + l16] of tile tq over this wave's dims
+  // half; the copies of tile `ctile` into its ring slot are issued between the k-steps.
+  auto qk = [&](int tq, f32x4 (&sacc)[2], int ctile) {
+    const DMLA_LDS char* tb = slot_of(tq);
+    int valid_rows;
+    const char* src = tile_src(ctile, valid_rows);
+    const unsigned dst = slot_addr(ctile);
+    sacc[0] = sacc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < kKcHalf; ++c) {
+      constexpr int c0 = kHalf * kKcHalf;
+      const int cc = c0 + c;
+      const int off = k_off[cc & 1] + (cc >> 1) * kGroupBytes;
+      const bf16x8 a = lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(tb + off));
+      sacc[0] = mfma_bf16(a, qreg[0][c], sacc[0]);
+      sacc[1] = mfma_bf16(a, qreg[1][c], sacc[1]);
+      // The copies refill the slot this wave's PV just read: its LDS reads must be complete.
+      if (c == 0) __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      if (c < 4) copy_part(c, src, valid_rows, dst);
+      if (c == 4 && ncopies > 4) copy_part(4, src, valid_rows, dst);
+    }
+  };
+  auto post_partial = [&](int tq, const f32x4 (&sacc)[2]) {
+    *reinterpret_cast<DMLA_LDS f32x4*>(xbuf + (tq & 1) * kXBytes + x_post) = sacc[1 - kHalf];
+  };
+  auto take_scores = [&](int tq, const f32x4 (&sacc)[2]) {
+    return sacc[kHalf] + *reinterpret_cast<const DMLA_LDS f32x4*>(xbuf + (tq & 1) * kXBytes + x_take);
+  };
+  auto masked = [&](int tq, const f32x4& s, float (&sr)[4]) {
+    const int key0 = tq * kTileN + 16 * kh + 4 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sr[i] = key0 + i > own_lim ? kNegInf : s[i];
+  };
+  // Max over both key halves of a per-row value (one LDS round trip; `slot` picks the buffer).
+  auto row_max_both_halves = [&](float v, int slot) {
+    rowx[(slot * 2 + kh) * kRowsPerWG + 16 * rb + l16] = v;
+    __syncthreads();
+    return fmaxf(v, rowx[(slot * 2 + (kh ^ 1)) * kRowsPerWG + 16 * rb + l16]);
+  };
 
-    if (tile_begin < tile_end) stage(tile_begin);
-    if (tile_begin + 1 < tile_end) stage(tile_begin + 1);
+  f32x4 sacc[2];
+#pragma unroll
+  for (int d = 0; d < kDbWave; ++d)
+#pragma unroll
+    for (int qg = 0; qg < 4; ++qg) oacc[d][qg] = f32x4{0.f, 0.f, 0.f, 0.f};
+  mtrue = kNegInf;
+  lsum = 0.f;
+  mref = kNegInf;
+  bool overflow = false;
+  int ovf_any = 0;
+  if (tile_begin < tile_end) {
+    if constexpr (kExact) {
+      // Scores-only pass for the exact row max (rows without any key keep -inf).
+      float mx = kNegInf;
+      stage(tile_begin, tile_begin);
+      for (int t = tile_begin; t < tile_end; ++t) {
+        wait_vmem();
+        __syncthreads();
+        qk(t, sacc, t + 1);
+        post_partial(t, sacc);
+        __syncthreads();
+        float sr[4];
+        masked(t, take_scores(t, sacc), sr);
+        mx = fmaxf(mx, fmaxf(fmaxf(sr[0], sr[1]), fmaxf(sr[2], sr[3])) * scale_log2);
+      }
+      wait_vmem();
+      mref_init = row_max_both_halves(group_max(mx), 1);
+      __syncthreads();
+    }
+
+    // Prologue: slot(t0-1) holds finite data (a copy of t0) and P(t0-1) = 0, so the PV of the
+    // first iteration adds nothing; slot(t0) holds t0; its partial scores are posted and the
+    // copy of t0+1 is in flight.  The fast path's reference max of each row is its max over
+    // tile t0 (every row with any key has one in the first tile of its work item).
+    stage(tile_begin, tile_begin - 1);
+    stage(tile_begin, tile_begin);
+    *reinterpret_cast<DMLA_LDS bf16x4*>(pbuf + ((tile_begin - 1) & 1) * kPBytes + p_post) = bf16x4{0.f, 0.f, 0.f, 0.f};
+    flags[wave] = 0;
+    wait_vmem();
+    __syncthreads();
+    qk(tile_begin, sacc, tile_begin + 1);
+    post_partial(tile_begin, sacc);
+    if constexpr (!kExact) {
+      __syncthreads();
+      float sr[4];
+      masked(tile_begin, take_scores(tile_begin, sacc), sr);
+      const float mhalf = group_max(fmaxf(fmaxf(sr[0], sr[1]), fmaxf(sr[2], sr[3])) * scale_log2);
+      mref = row_max_both_halves(mhalf, 0);
+    } else {
+      mref = mref_init;
+    }
+
+    // Iteration t: PV(t-1) and the partial scores of tile t+1 on the matrix cores with
+    // softmax(t) in between, then P(t) and the partials of t+1 are posted.  One barrier per
+    // tile.  Ring: PV reads slot(t-1), QK reads slot(t+1), slot(t) waits for PV(t), and each
+    // wave refills its own part of slot(t-1) with tile t+2 after its PV.
     for (int t = tile_begin; t < tile_end; ++t) {
-      wait_tile(t);
-      if (__syncthreads_or(overflow)) break;
-      if (t + 2 < tile_end) stage(t + 2);
-      const DMLA_LDS char* tb = lds + ((t - tile_begin) % kRing) * kTileBytes;
+      wait_vmem();       // this wave's copies of tile t+1 have landed
+      __syncthreads();   // partials(t), P(t-1), flags posted; tile t+1 complete
+      if constexpr (!kExact) {
+        const i32x4 f0 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags);
+        const i32x4 f1 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags + 4);
+        ovf_any = (f0[0] | f0[1] | f0[2] | f0[3]) | (f1[0] | f1[1] | f1[2] | f1[3]);
+        if (ovf_any != 0) break;
+      }
+      const f32x4 s = take_scores(t, sacc);
+      pv(t - 1);
+      qk(t + 1, sacc, t + 2);
 
-      // ---- partial S^T[key 16kb + 4g + i][pair row 16qg + l16] over this wave's dims half ----
-      f32x4 sacc[2][2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        sacc[kb][0] = sacc[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < kKcHalf; ++c) {
-          constexpr int c0 = kHalf * kKcHalf;
-          const int cc = c0 + c;
-          const int off = k_off[cc & 1] + (cc >> 1) * kGroupBytes + kb * 16 * 128;
-          const bf16x8 a = lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(tb + off));
-          sacc[kb][0] = mfma_bf16(a, qreg[0][c], sacc[kb][0]);
-          sacc[kb][1] = mfma_bf16(a, qreg[1][c], sacc[kb][1]);
-        }
-      }
-      pipeline_schedule<2 * kKcHalf, 1, kPrefetch>();
-      // Post the partner's rows, take ours: S of the own 16 rows summed over both dims halves.
-      DMLA_LDS char* xb = xbuf + (t & 1) * kXBytes;
-      *reinterpret_cast<DMLA_LDS f32x4*>(xb + x_post) = sacc[0][1 - kHalf];
-      *reinterpret_cast<DMLA_LDS f32x4*>(xb + x_post + 1024) = sacc[1][1 - kHalf];
-      __syncthreads();
-      const f32x4 s0 = sacc[0][kHalf] + *reinterpret_cast<const DMLA_LDS f32x4*>(xb + x_take);
-      const f32x4 s1 = sacc[1][kHalf] + *reinterpret_cast<const DMLA_LDS f32x4*>(xb + x_take + 1024);
-
-      // ---- online softmax of the own rows (exp2 domain) --------------------------------------
-      const int key0 = t * kTileN;
-      float x[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[i] = s0[i] * p.scale_log2;
-        x[4 + i] = s1[i] * p.scale_log2;
-      }
-      if (key0 + kTileN - 1 > wg_min_lim) {
-        const int lim = own_row < nrows ? limit_of(own_row) : -1;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          x[i] = key0 + 4 * g + i > lim ? kNegInf : x[i];
-          x[4 + i] = key0 + 16 + 4 * g + i > lim ? kNegInf : x[4 + i];
-        }
-      }
-      float mloc = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+      // ---- softmax of the own 16 rows x 16 keys (exp2 domain) ------------------------------
+      float sr[4];
+      masked(t, s, sr);
+      const float mloc = fmaxf(fmaxf(sr[0], sr[1]), fmaxf(sr[2], sr[3])) * scale_log2;  // scale > 0
       mtrue = fmaxf(mtrue, mloc);
-      // A row seeing its first finite scores adopts their group max as mref (its O and l are
-      // still zero); a row whose scores climb past mref + kHeadroom requests a restart.
-      if (__any(mref == kNegInf && mloc != kNegInf)) {
-        const float mt = group_max(mloc);
-        if (mref == kNegInf) mref = mt;
-      }
-      if (mloc > mref + kHeadroom) overflow = 1;
+      overflow = overflow || mloc > mref + kHeadroom;
       const float ms = mref == kNegInf ? 0.f : mref;
-      bf16x8 pk;  // keys {4g..4g+3, 16+4g..16+4g+3} of the own row
+      bf16x4 pk;  // keys 16 kh + 4g .. +3 of the own row
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float pv = fast_exp2(x[j] - ms);
-        lsum += pv;
-        pk[j] = (bf16)pv;
+      for (int j = 0; j < 4; ++j) {
+        const float pj = fast_exp2(__builtin_fmaf(sr[j], scale_log2, -ms));
+        lsum += pj;
+        pk[j] = (bf16)pj;
       }
-      *reinterpret_cast<DMLA_LDS bf16x8*>(pbuf + p_post) = pk;
-      __syncthreads();
-
-      // ---- O^T[dv][row] += V^T . P^T for this wave's 128 columns and all 64 rows -------------
-      bf16x8 pall[4];
-#pragma unroll
-      for (int qg = 0; qg < 4; ++qg) pall[qg] = *reinterpret_cast<const DMLA_LDS bf16x8*>(pbuf + qg * 1024 + lane * 16);
-#pragma unroll
-      for (int d = 0; d < kDbWave; ++d) {
-        const int base = v_off[d & 3] + (d >> 2) * kGroupBytes;
-        const bf16x4 v0 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tb + base));
-        const bf16x4 v1 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tb + base + 16 * 128));
-        const bf16x8 a = concat(v0, v1);
-#pragma unroll
-        for (int qg = 0; qg < 4; ++qg) oacc[d][qg] = mfma_bf16(a, pall[qg], oacc[d][qg]);
-      }
+      *reinterpret_cast<DMLA_LDS bf16x4*>(pbuf + (t & 1) * kPBytes + p_post) = pk;
+      if constexpr (!kExact) flags[wave] = __any(overflow) ? 1 : 0;
+      post_partial(t + 1, sacc);
+      iteration_schedule();
     }
     wait_vmem();
-    if (!__syncthreads_or(overflow)) break;
-    // Restart with every row's reference max raised to the largest score seen so far: tiles up
-    // to the overflowing one cannot overflow again, so each restart gets strictly further.
-    mref_init = fmaxf(mref_init, group_max(mtrue));
+    __syncthreads();     // P(end-1) posted (or the flags, after a break)
+    if constexpr (!kExact) {
+      if (ovf_any != 0) {
+        mqa_fwd_exact<kDecode, kHalf>(params, wk, lds, wave, lane);
+        return;
+      }
+    }
+    pv(tile_end - 1);
   }
 
   // ---- epilogue ---------------------------------------------------------------------------
+  // Row statistics over both key halves, then 1/l of all 64 rows for the output scaling.
   const bool poison = kDecode && __any(bad_page);
   const float nanv = __builtin_nanf("");
-  const float ltot = group_sum(lsum);
-  const float mt = group_max(mtrue);
-  if (g == 0) inv_l_lds[16 * wave + l16] = ltot > 0.f ? 1.f / ltot : 0.f;
-  // Statistics of the own rows.
-  if (g == 0 && own_row < nrows) {
+  const float lhalf = group_sum(lsum);
+  const float mhalf = group_max(mtrue);
+  rowx[(2 * 2 + kh) * kRowsPerWG + 16 * rb + l16] = lhalf;
+  rowx[(0 * 2 + kh) * kRowsPerWG + 16 * rb + l16] = mhalf;
+  __syncthreads();
+  const float ltot = lhalf + rowx[(2 * 2 + (kh ^ 1)) * kRowsPerWG + 16 * rb + l16];
+  const float mt = fmaxf(mhalf, rowx[(0 * 2 + (kh ^ 1)) * kRowsPerWG + 16 * rb + l16]);
+  __syncthreads();
+  DMLA_LDS float* inv_l = rowx + 1 * 2 * kRowsPerWG;  // [64 rows]
+  if (kh == 0) inv_l[16 * rb + l16] = ltot > 0.f ? 1.f / ltot : 0.f;
+  if (kh == 0 && g == 0 && own_row < nrows) {
     if constexpr (!kDecode) {
       if (p.m != nullptr) {
         const int pos = own_row / p.H, head = own_row - pos * p.H;
@@ -358,12 +439,12 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const Work& wk,
     }
   }
   __syncthreads();
-  const int col = 128 * wave + 4 * g;
+  const int col = 64 * wave + 4 * g;
 #pragma unroll
   for (int qg = 0; qg < 4; ++qg) {
     const int r = row0 + 16 * qg + l16;
     if (r >= nrows) continue;
-    const float inv = inv_l_lds[16 * qg + l16];
+    const float inv = inv_l[16 * qg + l16];
     if constexpr (!kDecode) {
       const int pos = r / p.H, head = r - pos * p.H;
       bf16* orp = p.o + b * p.o_sb + head * p.o_sh + pos * p.o_ss + col;
@@ -395,6 +476,26 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const Work& wk,
       }
     }
   }
+}
+
+// Out-of-line so the fast path carries none of its registers.  `params` is the kernel's
+// argument segment (MqaParams is the kernel's only argument), taken in the kernel itself: the
+// segment pointer is only defined inside kernels, and passing the parameters by reference
+// would copy them to scratch memory in every workgroup.
+template <bool kDecode, int kHalf>
+__device__ __noinline__ void mqa_fwd_exact(const MqaParams* params, Work wk, DMLA_LDS char* lds, int wave, int lane) {
+  // Call arguments arrive in VGPRs; the staging code needs the wave-uniform values in SGPRs.
+  const uint64_t pa = reinterpret_cast<uint64_t>(params);
+  const MqaParams& p = *reinterpret_cast<const MqaParams*>(
+      ((uint64_t)__builtin_amdgcn_readfirstlane((unsigned)(pa >> 32)) << 32) |
+      (unsigned)__builtin_amdgcn_readfirstlane((unsigned)pa));
+  wave = uniform(wave);
+  wk.b = uniform(wk.b); wk.row0 = uniform(wk.row0); wk.tile_begin = uniform(wk.tile_begin);
+  wk.tile_end = uniform(wk.tile_end); wk.split = uniform(wk.split); wk.nsplit = uniform(wk.nsplit);
+  wk.ctx = uniform(wk.ctx); wk.page_begin = uniform(wk.page_begin);
+  lds = reinterpret_cast<DMLA_LDS char*>(static_cast<uintptr_t>(uniform((int)lds_addr(lds))));
+  __syncthreads();
+  mqa_fwd_body<kDecode, kHalf, true>(p, &p, wk, lds, wave, lane);
 }
 
 template <bool kDecode>
@@ -443,8 +544,9 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
       page_cache[i] = p.block_table[wk.b * p.bt_sb + wk.page_begin + i];
     __syncthreads();
   }
-  if ((wave & 1) == 0) mqa_fwd_body<kDecode, 0>(p, wk, lds, wave, lane);
-  else mqa_fwd_body<kDecode, 1>(p, wk, lds, wave, lane);
+  const MqaParams* params = (const MqaParams*)(__builtin_amdgcn_kernarg_segment_ptr());
+  if (((wave >> 1) & 1) == 0) mqa_fwd_body<kDecode, 0, false>(p, params, wk, lds, wave, lane);
+  else mqa_fwd_body<kDecode, 1, false>(p, params, wk, lds, wave, lane);
 }
 
 // Merges the normalised split partials of one (sequence, head): o = sum_s w_s o_s / sum_s w_s
