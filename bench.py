@@ -205,8 +205,8 @@ def cpu_decode(q, pool, table, lens, bytes_total):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--secondary", default="decode", help="comma list of extra workloads: decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()

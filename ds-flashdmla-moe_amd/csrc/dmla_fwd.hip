@@ -53,7 +53,7 @@ constexpr int kXOffset = kRing * kTileBytes;
 constexpr int kPOffset = kXOffset + 2 * kXBytes;
 constexpr int kRowOffset = kPOffset + 2 * kPBytes;  // per-row exchange [3][2 key halves][64]
 constexpr int kFlagOffset = kRowOffset + 3 * 2 * kRowsPerWG * 4;
-constexpr int kPageOffset = kFlagOffset + kWaves * 4;
+constexpr int kPageOffset = kFlagOffset + 2 * kWaves * 4;
 constexpr int kLdsBytes = kPageOffset + kMaxSplitPages * 4;
 constexpr float kHeadroom = 32.0f;                  // log2 headroom of p over the reference max
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
@@ -345,7 +345,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     stage(tile_begin, tile_begin - 1);
     stage(tile_begin, tile_begin);
     *reinterpret_cast<DMLA_LDS bf16x4*>(pbuf + ((tile_begin - 1) & 1) * kPBytes + p_post) = bf16x4{0.f, 0.f, 0.f, 0.f};
-    flags[wave] = 0;
+    flags[((tile_begin - 1) & 1) * kWaves + wave] = 0;
     wait_vmem();
     __syncthreads();
     qk(tile_begin, sacc, tile_begin + 1);
@@ -367,11 +367,13 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     for (int t = tile_begin; t < tile_end; ++t) {
       wait_vmem();       // this wave's copies of tile t+1 have landed
       __syncthreads();   // partials(t), P(t-1), flags posted; tile t+1 complete
+      // Overflow flags of tile t-1 are read now but acted on at the end of the iteration, so
+      // their LDS round trip stays off the critical path (the extra tile's work is discarded).
+      // Double-buffered by tile parity: every wave reads the same values before anyone writes.
+      i32x4 f0 = {0, 0, 0, 0}, f1 = {0, 0, 0, 0};
       if constexpr (!kExact) {
-        const i32x4 f0 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags);
-        const i32x4 f1 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags + 4);
-        ovf_any = (f0[0] | f0[1] | f0[2] | f0[3]) | (f1[0] | f1[1] | f1[2] | f1[3]);
-        if (ovf_any != 0) break;
+        f0 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags + ((t - 1) & 1) * kWaves);
+        f1 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags + ((t - 1) & 1) * kWaves + 4);
       }
       const f32x4 s = take_scores(t, sacc);
       pv(t - 1);
@@ -392,13 +394,22 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
         pk[j] = (bf16)pj;
       }
       *reinterpret_cast<DMLA_LDS bf16x4*>(pbuf + (t & 1) * kPBytes + p_post) = pk;
-      if constexpr (!kExact) flags[wave] = __any(overflow) ? 1 : 0;
       post_partial(t + 1, sacc);
       iteration_schedule();
+      if constexpr (!kExact) {
+        ovf_any = (f0[0] | f0[1] | f0[2] | f0[3]) | (f1[0] | f1[1] | f1[2] | f1[3]);
+        flags[(t & 1) * kWaves + wave] = __any(overflow) ? 1 : 0;
+        if (ovf_any != 0) break;
+      }
     }
     wait_vmem();
-    __syncthreads();     // P(end-1) posted (or the flags, after a break)
+    __syncthreads();     // P(end-1) and the flags of the last tile posted (or a break)
     if constexpr (!kExact) {
+      if (ovf_any == 0) {  // the last tile's flags were never read inside the loop
+        const i32x4 f0 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags + ((tile_end - 1) & 1) * kWaves);
+        const i32x4 f1 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags + ((tile_end - 1) & 1) * kWaves + 4);
+        ovf_any = (f0[0] | f0[1] | f0[2] | f0[3]) | (f1[0] | f1[1] | f1[2] | f1[3]);
+      }
       if (ovf_any != 0) {
         mqa_fwd_exact<kDecode, kHalf>(params, wk, lds, wave, lane);
         return;

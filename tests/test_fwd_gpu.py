@@ -77,6 +77,21 @@ def test_fwd_score_growth_takes_the_exact_max_pass(gpu):
 
 
 @pytest.mark.gpu
+def test_fwd_score_jump_in_the_last_tile(gpu):
+    # Keys of the last 32-key tile score ~86 (log2 units) above all earlier keys: only rows
+    # that reach that tile overflow, and only there -- the restart must still be taken.
+    B, H, S = 1, 16, 256
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(B, H, S, 576, generator=g) * 0.1
+    k = torch.randn(B, S, 576, generator=g) * 0.1
+    q[..., 512] = 4.0
+    k[..., 512] = 0.0
+    k[:, S - 32:, 512] = 30.0
+    q, k = q.to(torch.bfloat16), k.to(torch.bfloat16)
+    _check(gpu, q, k, True, scale=0.5)
+
+
+@pytest.mark.gpu
 def test_fwd_config2_full_shape(gpu):
     # B=4, H=16, S=2048, 576/512, N(0,1)*0.5, scale 1/sqrt(192), causal.
     q, k = _inputs(4, 16, 2048, 2048, seed=2)
