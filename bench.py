@@ -11,8 +11,8 @@ counting B*H*S(S+1)*(576+512) flops (unmasked causal pairs only).
 
 `roofline` times the kernel itself with HIP events recorded on the stream it is launched on;
 `traffic` comes from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary when present.
-`cpu_baseline` times the fp32 PyTorch eager oracle (oracle/dmla_ref.py) on the host cores on
-a bounded sample of the same workload.  `secondary` carries the paged decode (config 3) in
+`cpu_baseline` times the fp32 PyTorch eager oracle (oracle/dmla_ref.py) on the host cores
+(at most 16 threads) over the same workload, repeated for about --cpu-seconds seconds.  `secondary` carries the paged decode (config 3) in
 KV GB/s with its own HBM roofline, timed the same way with rotating KV pools larger than the
 256 MB MALL.
 """
@@ -102,29 +102,46 @@ def bench_prefill(steps, warmup, cpu_baseline):
                      "algorithmic_flops_per_launch": flops},
     }
     if cpu_baseline:
-        res["cpu_baseline"] = cpu_prefill(q.cpu(), k.cpu())
+        res["cpu_baseline"] = cpu_prefill(q.cpu(), k.cpu(), cpu_baseline)
     return res
 
 
-def cpu_prefill(q, k):
-    """fp32 eager oracle on a bounded sample: batch element 0 (all 16 heads, S=2048)."""
+def _cpu_threads():
+    """Host threads for the CPU baseline: the cores this process may run on, at most 16 (the
+    GPU box's CPU share)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def _time_repeated(fn, budget_s):
+    """Calls fn() until at least budget_s seconds have passed; returns (calls, seconds)."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        t = time.perf_counter() - t0
+        if t >= budget_s:
+            return n, t
+
+
+def cpu_prefill(q, k, budget_s):
+    """fp32 eager oracle over the whole config-2 batch, repeated for about budget_s seconds."""
     import torch
 
     from oracle import dmla_ref as R
 
-    torch.set_num_threads(os.cpu_count() or 1)
-    qs, ks = q[:1].float(), k[:1].float()
-    S, H = qs.shape[2], qs.shape[1]
-    flops = H * S * (S + 1) * (576 + 512)
-    R.dmla_fwd_cache_latent(qs[:, :, :256], ks[:, :256], 512, SCALE, True)  # warm-up
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        R.dmla_fwd_cache_latent(qs, ks, 512, SCALE, True)
-        times.append(time.perf_counter() - t0)
-    t = sorted(times)[1]
-    return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": "config 2 batch element 0 (16 heads x 2048 causal), fp32 eager oracle, median of 3",
+    torch.set_num_threads(_cpu_threads())
+    qs, ks = q.float(), k.float()
+    B, H, S = qs.shape[0], qs.shape[1], qs.shape[2]
+    flops = B * H * S * (S + 1) * (576 + 512)
+    R.dmla_fwd_cache_latent(qs[:1, :, :256], ks[:1, :256], 512, SCALE, True)  # warm-up
+    n, t = _time_repeated(lambda: R.dmla_fwd_cache_latent(qs, ks, 512, SCALE, True), budget_s)
+    return {"value": n * flops / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"all of config 2 ({B}x{H} heads x {S} causal) through the fp32 eager oracle, "
+                      f"{n} passes in {t:.1f} s",
             "seconds": t}
 
 
@@ -177,29 +194,41 @@ def bench_decode(steps, warmup, cpu_baseline):
                      "algorithmic_bytes_per_launch": bytes_total},
     }
     if cpu_baseline:
-        res["cpu_baseline"] = cpu_decode(q.cpu(), pools[0].cpu(), tables[0].cpu(), lens.to(torch.int32), bytes_total)
+        res["cpu_baseline"] = cpu_decode(q.cpu(), pools[0].cpu(), tables[0].cpu(), lens.to(torch.int32), bytes_total,
+                                         cpu_baseline)
     return res
 
 
-def cpu_decode(q, pool, table, lens, bytes_total):
-    """fp32 eager oracle (gather through the block table + attention) on 8 of the 64 sequences."""
+def cpu_decode(q, pool, table, lens, bytes_total, budget_s):
+    """fp32 eager oracle (gather through the block table + attention) over all 64 sequences,
+    repeated for about budget_s seconds."""
     import torch
 
     from oracle import dmla_ref as R
 
-    torch.set_num_threads(os.cpu_count() or 1)
-    n = 8
-    sample_bytes = bytes_total * float(lens[:n].sum()) / float(lens.sum())
-    R.dmla_decode_paged(q[:1].float(), pool, table[:1], lens[:1], 512, SCALE)  # warm-up
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        R.dmla_decode_paged(q[:n].float(), pool, table[:n], lens[:n], 512, SCALE)
-        times.append(time.perf_counter() - t0)
-    t = sorted(times)[1]
-    return {"value": sample_bytes / t / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"config 3 sequences 0..{n - 1} (ctx sum {int(lens[:n].sum())}), fp32 eager oracle, median of 3",
+    torch.set_num_threads(_cpu_threads())
+    qf = q.float()
+    R.dmla_decode_paged(qf[:1], pool, table[:1], lens[:1], 512, SCALE)  # warm-up
+    n, t = _time_repeated(lambda: R.dmla_decode_paged(qf, pool, table, lens, 512, SCALE), budget_s)
+    return {"value": n * bytes_total / t / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"all of config 3 ({q.shape[0]} sequences, ctx sum {int(lens.sum())}) through the fp32 "
+                      f"eager oracle, {n} passes in {t:.1f} s",
             "seconds": t}
+
+
+def copy_calibration(mib):
+    """Streaming copies of `mib` MiB for calibrating the HBM byte counters.  torch's elementwise
+    negation kernel is a plain copy (it reads N bytes and writes N bytes), so FETCH_SIZE and
+    WRITE_SIZE of its dispatches give the counters' scale for the kernels' traffic figures."""
+    import torch
+
+    n = mib * 1024 * 1024
+    src = torch.randn(n // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "launches": 5}))
 
 
 def main():
@@ -209,6 +238,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--secondary", default="decode", help="comma list of extra workloads: decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget per workload")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run MIB-sized device copies (HBM counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs and reports the "
@@ -220,7 +252,10 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
-    cpu = not args.no_cpu_baseline
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
+    cpu = 0.0 if args.no_cpu_baseline else args.cpu_seconds
     primary = bench_prefill(args.steps, args.warmup, cpu)
     secondary = {}
     for name in [s for s in args.secondary.split(",") if s]:

@@ -72,6 +72,37 @@ __device__ __forceinline__ bf16x8 concat(const bf16x4& a, const bf16x4& b) {
   return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// LDS tile layout shared by every kernel that stages a 32-row bf16 tile (keys, queries or
+// output gradients): [chunk group (64 columns, 128 B)][row (32)][8 sixteen-byte chunks], so rows
+// 2k and 2k+1 fall in opposite halves of the 64 x 4-byte banks.  The chunk at logical position
+// j of row r sits at physical position j ^ swz(r & 15), where swz maps the 8 rows of either
+// bank half bijectively onto 0..7 and keeps the pair index (bits 1-2) distinct across 4
+// consecutive same-half rows.  Both operand reads are then conflict-free: 16 lanes reading one
+// 16-byte chunk of rows r..r+15 (b128 row operand) and 32 lanes reading 32-byte column pairs of
+// rows r..r+7 (ds_read_b64_tr_b16 column operand).
+__host__ __device__ constexpr int swz(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
+constexpr int kTileRows = 32;                 // rows of a staged tile
+constexpr int kGroupBytes = kTileRows * 128;  // one 64-column chunk group of a tile (4 KB)
+
+// Byte offset in a staged tile of the 16-byte chunk holding columns 8*chunk .. 8*chunk+7 of
+// tile row `row`.
+__device__ __forceinline__ int tile_chunk_off(int row, int chunk) {
+  return (chunk >> 3) * kGroupBytes + row * 128 + 16 * ((chunk & 7) ^ swz(row & 15));
+}
+// Per-lane byte offset of a b128 row-operand read (MFMA A or B operand with k along columns):
+// lane l reads row 16*rb + l%16, columns 32*c + 8*(l/16) .. +7.
+__device__ __forceinline__ int row_operand_off(int lane, int rb, int c) {
+  return tile_chunk_off(16 * rb + (lane & 15), 4 * c + (lane >> 4));
+}
+// Per-lane byte offset of a ds_read_b64_tr_b16 column-operand read (MFMA operand with k along
+// rows): lane 4e+q of group g reads row 4g+e (+16 for the second half), columns
+// 16*cb + 4q .. +3; the hardware hands lane j of the group column 16*cb + j for 4 rows.
+__device__ __forceinline__ int col_operand_off(int lane, int cb, int half) {
+  const int g = lane >> 4, e = (lane & 15) >> 2, q = lane & 3;
+  const int row = 16 * half + 4 * g + e;
+  return tile_chunk_off(row, 2 * cb + (q >> 1)) + 8 * (q & 1);
+}
+
 // Reductions over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48: the lanes that
 // share one MFMA column) with the gfx950 row-swap instructions.  Called with the same value in
 // both operands, permlane16_swap / permlane32_swap return, in some order, a lane's value and

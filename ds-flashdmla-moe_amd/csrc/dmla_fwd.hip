@@ -38,7 +38,6 @@ constexpr int kDv = 512;
 constexpr int kPage = 64;                           // decode page size (tokens)
 constexpr int kTileN = 32;                          // keys per LDS tile
 constexpr int kGroups = kDqk / 64;                  // 9 chunk groups of 64 columns (128 B)
-constexpr int kGroupBytes = kTileN * 128;           // 4 KB: one chunk group of all tile rows
 constexpr int kTileBytes = kGroups * kGroupBytes;   // 36 KB
 constexpr int kRing = 3;                            // ring slots
 constexpr int kWaves = 8;
@@ -58,16 +57,8 @@ constexpr int kLdsBytes = kPageOffset + kMaxSplitPages * 4;
 constexpr float kHeadroom = 32.0f;                  // log2 headroom of p over the reference max
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 static_assert(kPage % kTileN == 0, "a page holds whole tiles");
+static_assert(kTileN == kTileRows, "key tiles use the shared 32-row tile layout");
 static_assert(kGroups == kWaves + 1, "each wave copies its PV chunk group; the rope group is shared");
-
-// LDS tile layout: [chunk group cg (9)][row (32)][8 sixteen-byte chunks], 128 B per row slice,
-// so rows 2k and 2k+1 fall in opposite halves of the 64 x 4-byte banks.  The chunk at logical
-// position j of row r sits at physical position j ^ swz(r & 15), where swz maps the 8 rows of
-// either bank half bijectively onto 0..7 and keeps the pair index (bits 1-2) distinct across
-// 4 consecutive same-half rows.  Both operand reads are then conflict-free: 16 lanes reading
-// one 16-byte chunk of rows r..r+15 (b128 K operand) and 32 lanes reading 32-byte column pairs
-// of rows r..r+7 (ds_read_b64_tr_b16 V operand).
-__host__ __device__ constexpr int swz(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
 
 // Scheduling template of one pipelined tile iteration: 22 LDS operand reads (partials, P, V,
 // K) feeding 34 MFMAs, with vector ALU work slotted between them.  A few reads run ahead; the
