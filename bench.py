@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Flash-DMLA benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--secondary prefill,decode] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--secondary decode,bwd] [--no-cpu-baseline]
 
 Primary line (BASELINE.json metric, config 2): cache-latent DMLA prefill forward, bf16, causal,
 B=4, H=16, S=2048, Q [B,H,S,576], shared K_lat [B,S,576], V_lat = K_lat[..., :512], scale
@@ -12,9 +12,10 @@ counting B*H*S(S+1)*(576+512) flops (unmasked causal pairs only).
 `roofline` times the kernel itself with HIP events recorded on the stream it is launched on;
 `traffic` comes from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary when present.
 `cpu_baseline` times the fp32 PyTorch eager oracle (oracle/dmla_ref.py) on the host cores
-(at most 16 threads) over the same workload, repeated for about --cpu-seconds seconds.  `secondary` carries the paged decode (config 3) in
-KV GB/s with its own HBM roofline, timed the same way with rotating KV pools larger than the
-256 MB MALL.
+(at most 16 threads) over the same workload, repeated for about --cpu-seconds seconds.
+`secondary` carries the paged decode (config 3) in KV GB/s with its own HBM roofline, timed
+the same way with rotating KV pools larger than the 256 MB MALL, and the cache-latent backward
+(config 5) in TFLOP/s, counting B*H*S(S+1)*(3*576+2*512) flops.
 """
 import argparse
 import json
@@ -216,6 +217,56 @@ def cpu_decode(q, pool, table, lens, bytes_total, budget_s):
             "seconds": t}
 
 
+def bench_bwd(steps, warmup, cpu_baseline):
+    """Config 5: cache-latent backward (all its kernels) from one forward's saved o, m, l."""
+    import torch
+
+    from python import ops
+
+    B, H, S = 4, 16, 2048
+    dev = torch.device("cuda:0")
+    q = _seeded((B, H, S, 576), 0, 0.5, torch.bfloat16).to(dev)
+    k = _seeded((B, S, 576), 1, 0.5, torch.bfloat16).to(dev)
+    do = _seeded((B, H, S, 512), 2, 1.0, torch.bfloat16).to(dev)
+    o, m, l = ops.flash_dmla_fwd(q, k, 512, SCALE, True)
+    flops = B * H * S * (S + 1) * (3 * 576 + 2 * 512)
+
+    def step(i=0):
+        ops.flash_dmla_bwd(q, k, o, do, m, l, 512, SCALE, True)
+
+    wall_ms, kern_ms = _time_launches(step, steps, warmup)
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    res = {
+        "metric": "DMLA backward TFLOP/s (cache-latent, config 5)",
+        "value": flops / (wall_ms * 1e-3) / 1e12,
+        "unit": "TFLOP/s",
+        "ms_per_step": wall_ms,
+        "config": {"workload": "cache-latent backward (BASELINE config 5)", "batch": B, "heads": H, "seq_len": S,
+                   "d_qk": 576, "d_v": 512, "causal": True, "softmax_scale": SCALE},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": _load_traffic("bwd"),
+                     "kernel": "bwd_prep + bwd_kt + bwd_dkdv + bwd_dq + bwd_dk_reduce", "kernel_ms": kern_ms,
+                     "algorithmic_flops_per_launch": flops},
+    }
+    if cpu_baseline:
+        res["cpu_baseline"] = cpu_bwd(q.cpu(), k.cpu(), o.cpu(), do.cpu(), m.cpu(), l.cpu(), flops, cpu_baseline)
+    return res
+
+
+def cpu_bwd(q, k, o, do, m, l, flops, budget_s):
+    """fp32 eager closed-form oracle backward over all of config 5, repeated for ~budget_s s."""
+    import torch
+
+    from oracle import dmla_ref as R
+
+    torch.set_num_threads(_cpu_threads())
+    qf, kf, of, dof = q.float(), k.float(), o.float(), do.float()
+    n, t = _time_repeated(lambda: R.dmla_bwd_cache_latent(qf, kf, of, dof, m, l, 512, SCALE, True), budget_s)
+    return {"value": n * flops / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"all of config 5 through the fp32 eager oracle backward, {n} passes in {t:.1f} s",
+            "seconds": t}
+
+
 def copy_calibration(mib):
     """Streaming copies of `mib` MiB for calibrating the HBM byte counters.  torch's elementwise
     negation kernel is a plain copy (it reads N bytes and writes N bytes), so FETCH_SIZE and
@@ -236,7 +287,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=30)
-    ap.add_argument("--secondary", default="decode", help="comma list of extra workloads: decode")
+    ap.add_argument("--secondary", default="decode,bwd", help="comma list of extra workloads: decode, bwd")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget per workload")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -261,6 +312,8 @@ def main():
     for name in [s for s in args.secondary.split(",") if s]:
         if name == "decode":
             secondary["decode"] = bench_decode(args.steps, args.warmup, cpu)
+        elif name == "bwd":
+            secondary["bwd"] = bench_bwd(args.steps, args.warmup, cpu)
         else:
             raise SystemExit(f"unknown secondary workload {name}")
     line = {

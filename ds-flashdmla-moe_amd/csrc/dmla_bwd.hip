@@ -1,0 +1,638 @@
+// Cache-latent DMLA backward for gfx950 from the saved row statistics m and l.
+//
+// What it computes is the intended FA2 backward of csrc/attention/fa2_bwd.cu:198-310 (D_i =
+// rowsum(dO_i * O_i), dS = P * (dP - D), dV += P^T dO, dK += dS^T Q, dQ += dS K) applied to
+// the DMLA cache-latent layout of README.md:12-15: one latent K_lat[b] shared by every head and
+// V_lat = K_lat[..., :512], so
+//     dQ      = scale * dS K_lat
+//     dK_lat  = scale * sum_heads dS^T Q  +  [sum_heads P^T dO, 0]
+// with P = exp(scale q.k - m) / l rebuilt from the forward's statistics (README.md:12).
+//
+// Rows are (query position, head) pairs with the head fastest, as in the forward, so the 16
+// heads of a position share one causal key range.  Five kernels run in order on one stream:
+//   bwd_prep_kernel       per row: lse2 = (m + ln l) log2(e) and D = rowsum(dO * O);
+//   bwd_kt_kernel         K_lat^T in fp16 (dims x keys, zero padded): the B operand of dQ = dS' K;
+//   bwd_dkdv_kernel       per 64-key block, streaming 32-row tiles: S, P, dP and dS' = scale dS
+//                         on MFMA, dK_lat accumulated in registers (V fold included), dS'
+//                         written once to HBM as fp16 16x16 blocks;
+//   bwd_dq_kernel         dQ = dS' K_lat per 64-row tile over its causal key range;
+//   bwd_dk_reduce_kernel  sums the dK_lat partials of the row segments in a fixed order.
+// No atomics anywhere: the result is bitwise deterministic.
+//
+// Operand precision: S = Q K^T and dP = dO V^T multiply the bf16 inputs as they are.  The
+// second-stage products dS'^T Q, P^T dO and dS' K take fp16 operands: P and dS' are rounded to
+// fp16 (11-bit significand) instead of bf16 (8-bit), and Q, dO, K_lat are converted to fp16
+// exactly.  A key that every later row of every head attends to sums thousands of such terms;
+// with bf16 P and dS' that rounding alone costs ~1e-3 of |dK_lat| (2e-2 at the config-5
+// magnitudes of ~20), with fp16 an eighth of it -- within a few 1e-3 of exact fp32 operands.
+#include "dmla_common.h"
+#include "dmla_host.h"
+
+namespace dmla {
+namespace {
+
+constexpr int kDqk = 576;
+constexpr int kDv = 512;
+constexpr int kKeys = 64;                           // keys per dK/dV work block
+constexpr int kRows = kTileRows;                    // rows per staged row tile (32)
+constexpr int kBwdThreads = 256;                    // 4 waves, one per SIMD
+constexpr int kQGroups = kDqk / 64;                 // 9 chunk groups of a Q tile
+constexpr int kOGroups = kDv / 64;                  // 8 chunk groups of a dO tile
+constexpr int kQBytes = kQGroups * kGroupBytes;     // 36 KB
+constexpr int kStageBytes = kQBytes + kOGroups * kGroupBytes;   // 68 KB: Q and dO of one tile
+constexpr int kXOffset = 2 * kStageBytes;           // P^T / dS'^T exchange: [2][4 kb][64 lanes][16 B]
+constexpr int kDkdvLds = kXOffset + 2 * 4 * 1024;   // 144 KB
+constexpr int kCb = kDqk / 16;                      // 36 column blocks of dK / dQ
+constexpr int kPartFloats = kKeys * kDqk;           // one dK partial: 64 keys x 576 fp32
+constexpr int kMaxParts = 64;
+// dQ kernel: stage = dS' blocks of 64 rows x 32 keys (4 KB) + K^T of 576 dims x 32 keys (36 KB)
+constexpr int kDqDsBytes = 4096;
+constexpr int kDqStageBytes = kDqDsBytes + kDqk * 64;
+constexpr int kDqLds = 2 * kDqStageBytes;           // 80 KB
+static_assert(kDkdvLds <= 160 * 1024 && kDqLds <= 160 * 1024, "LDS budget");
+
+struct BwdParams {
+  const bf16* q;
+  const bf16* k;
+  const bf16* o;
+  const bf16* dout;
+  const float* m;       // [B, H, Sq] contiguous
+  const float* l;
+  void* dq;
+  void* dk;
+  int dq_fp32, dk_fp32;
+  int64_t q_sb, q_sh, q_ss, k_sb, k_ss, o_sb, o_sh, o_ss, do_sb, do_sh, do_ss;
+  int64_t dq_sb, dq_sh, dq_ss, dk_sb, dk_ss;
+  int B, H, Sq, Sk, causal;
+  float scale, scale_log2;
+  int R;                // H * Sq rows per batch element
+  int n_rt;             // 32-row tiles per batch element, even: 2 * ceil(R / 64)
+  int n_kb;             // 64-key blocks: ceil(Sk / 64)
+  int n_pairs;          // ceil(n_kb / 2)
+  int parts;            // row segments per key-block pair
+  int n_items;          // B * n_pairs * parts
+  int kt_ld;            // K^T row length (keys): 64 * n_kb
+  float2* lsed;         // [B][32 n_rt] (lse2, D); padding rows hold (+inf, 0)
+  _Float16* kt;         // [B][576][kt_ld] fp16
+  _Float16* ds;         // [B][2 n_rt row blocks][4 n_kb key blocks][256]: fp16 dS' 16x16 blocks, MFMA C order
+  float* part;          // [n_items][2][4 kb][36 cb][64 lanes][4]: dK_lat partials in MFMA C order
+};
+
+// ---- work split of the dK/dV kernel, shared by the host and the reduction ------------------
+// Key block kb needs the row tiles from first_row_tile(kb) on (causal: rows whose position can
+// see key 64 kb), rounded down to an even tile so that every 64-row dQ tile that reads a dS'
+// block of kb finds it written.  Blocks kb and n_kb-1-kb form a pair: the first is walked from
+// the last row tile down, the second from its first row tile up, so every pair has about the
+// same length and, at any moment, all pairs of a batch element read the same one or two row
+// tiles (L2 sharing).  Each pair's steps are cut into `parts` equal segments.
+__host__ __device__ inline int first_row_tile(int causal, int Sq, int Sk, int H, int kb) {
+  if (!causal) return 0;
+  const int first_pos = max(0, kKeys * kb - (Sk - Sq));
+  return 2 * (int)(((int64_t)first_pos * H) / 64);
+}
+struct PairPlan {
+  int kb_a, kb_b, steps_a, total;
+};
+__host__ __device__ inline PairPlan pair_plan(int causal, int Sq, int Sk, int H, int n_rt, int n_kb, int i) {
+  PairPlan pp;
+  pp.kb_a = i;
+  pp.kb_b = n_kb - 1 - i;
+  pp.steps_a = n_rt - first_row_tile(causal, Sq, Sk, H, pp.kb_a);
+  pp.total = pp.steps_a + (pp.kb_b != pp.kb_a ? n_rt - first_row_tile(causal, Sq, Sk, H, pp.kb_b) : 0);
+  return pp;
+}
+__host__ __device__ inline int part_begin(int total, int parts, int j) {
+  return (int)(((int64_t)total * j) / parts);
+}
+
+__device__ __forceinline__ f16x4 to_f16x4(float a, float b, float c, float d) {
+  f16x4 r;
+  r[0] = (_Float16)a; r[1] = (_Float16)b; r[2] = (_Float16)c; r[3] = (_Float16)d;
+  return r;
+}
+
+// ---- 1. row statistics -------------------------------------------------------------------
+// One workgroup per 32-row tile; 8 lanes per row, each summing 64 products of dO * O.
+__global__ void __launch_bounds__(256) bwd_prep_kernel(BwdParams p) {
+  const int b = blockIdx.y;
+  const int t = threadIdx.x;
+  const int row = blockIdx.x * kRows + (t >> 3);
+  const int part = t & 7;
+  float dsum = 0.f;
+  int pos = 0, h = 0;
+  const bool valid = row < p.R;
+  if (valid) {
+    pos = row / p.H;
+    h = row - pos * p.H;
+    const bf16* orow = p.o + b * p.o_sb + h * p.o_sh + pos * p.o_ss + 64 * part;
+    const bf16* drow = p.dout + b * p.do_sb + h * p.do_sh + pos * p.do_ss + 64 * part;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const bf16x8 ov = *reinterpret_cast<const bf16x8*>(orow + 8 * c);
+      const bf16x8 dv = *reinterpret_cast<const bf16x8*>(drow + 8 * c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dsum += (float)ov[e] * (float)dv[e];
+    }
+  }
+  dsum += __shfl_xor(dsum, 1, 8);
+  dsum += __shfl_xor(dsum, 2, 8);
+  dsum += __shfl_xor(dsum, 4, 8);
+  if (part == 0) {
+    float lse2 = __builtin_inff();
+    if (valid) {
+      const int64_t idx = ((int64_t)b * p.H + h) * p.Sq + pos;
+      const float mv = p.m[idx], lv = p.l[idx];
+      // Rows that see no key (l = 0) get +inf, so that P = exp2(s - lse2) = 0 everywhere.
+      if (lv > 0.f && __builtin_isfinite(mv)) lse2 = (mv + __logf(lv)) * kLog2e;
+    } else {
+      dsum = 0.f;
+    }
+    p.lsed[(int64_t)b * p.n_rt * kRows + row] = make_float2(lse2, dsum);
+  }
+}
+
+// ---- 2. K_lat^T ----------------------------------------------------------------------------
+// One workgroup per (64 keys, 64 dims) block through an LDS transpose; keys >= Sk are zero.
+// The bf16 -> fp16 conversion is exact for |K| in fp16's normal range.
+__global__ void __launch_bounds__(256) bwd_kt_kernel(BwdParams p) {
+  __shared__ _Float16 tile[64][64 + 8];
+  const int b = blockIdx.z, kb = blockIdx.y, db = blockIdx.x;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int idx = t + 256 * r;
+    const int key = idx >> 3, c = idx & 7;
+    const int gk = kb * 64 + key;
+    bf16x8 v = {};
+    if (gk < p.Sk) v = *reinterpret_cast<const bf16x8*>(p.k + b * p.k_sb + gk * p.k_ss + 64 * db + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[key][8 * c + e] = (_Float16)(float)v[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int idx = t + 256 * r;
+    const int d = idx >> 3, c = idx & 7;
+    f16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = tile[8 * c + e][d];
+    *reinterpret_cast<f16x8*>(p.kt + ((int64_t)b * kDqk + 64 * db + d) * p.kt_ld + kb * 64 + 8 * c) = v;
+  }
+}
+
+// ---- 3. dK_lat / dV: key-block-stationary sweep over row tiles ----------------------------
+//
+// Workgroup = 4 waves (one per SIMD, up to 512 registers each) on 64 keys.  Per 32-row tile:
+//   S-phase:  wave w computes S and dP for rows 16 (w&1) .. +15 and keys 32 (w>>1) .. +31
+//             (2 x 34 MFMAs), with those keys' K_lat rows held in registers as the B operand
+//             and the rows' Q / dO read from LDS; then P and dS' = scale P (dP - D), masked.
+//             The MFMA C layout (lane: one key, 4 rows) is exactly half of the A operand the
+//             dK update needs (lane: one key, 8 rows), so the two row halves meet in a 4 KB LDS
+//             exchange without any transposition.  dS' also goes to HBM for dQ.
+//   dK-phase: wave w owns column blocks w, w+4, .., w+32 of all 64 keys (36 accumulators):
+//             dK += dS'^T Q (9 blocks) and dK[:, :512] += P^T dO (8 blocks), fp16 operands; Q
+//             and dO columns come from ds_read_b64_tr_b16 so that k runs along the tile's rows.
+// Row tiles stream through two LDS stages (Q + dO = 68 KB each) with direct global->LDS copies;
+// two barriers per tile (tile landed / exchange written).
+__global__ void __launch_bounds__(kBwdThreads, 1) bwd_dkdv_kernel(BwdParams p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kDkdvLds];
+  DMLA_LDS char* lds = (DMLA_LDS char*)smem;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int lane = lane_id();
+  // Consecutive work items share (batch, segment) and so read the same row tiles: keep them on
+  // one XCD (workgroups are dealt to the 8 XCDs round robin).
+  const int per_xcd = (p.n_items + 7) >> 3;
+  const int u = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+  if (u >= p.n_items) return;
+  const int pi = u % p.n_pairs;
+  const int pj = (u / p.n_pairs) % p.parts;
+  const int b = u / (p.n_pairs * p.parts);
+  const PairPlan pp = pair_plan(p.causal, p.Sq, p.Sk, p.H, p.n_rt, p.n_kb, pi);
+  const int lo = part_begin(pp.total, p.parts, pj), hi = part_begin(pp.total, p.parts, pj + 1);
+
+  const int l16 = lane & 15, g = lane >> 4;
+  const int rb = wave & 1;       // S-phase row block
+  const int kp = wave >> 1;      // S-phase key pair: key blocks 2 kp, 2 kp + 1 of the 64
+  const int off = p.Sk - p.Sq;
+  const float scale = p.scale, scale_log2 = p.scale_log2;
+  const unsigned lds_base = lds_addr(lds);
+  DMLA_LDS char* xbuf = lds + kXOffset;
+
+  // Per-lane LDS offsets (tile-relative).  S-phase A operand (row operand of row block rb):
+  // chunk 4c + g of row 16 rb + l16 = group c/2, in-group chunk 4 (c&1) + g.
+  const int arow = 16 * rb + l16;
+  const int a_off0 = arow * 128 + 16 * (g ^ swz(arow & 15));
+  const int a_off1 = arow * 128 + 16 * ((4 + g) ^ swz(arow & 15));
+  // dK-phase B operand (column operand) of column block cb = wave + 4u: group u, in-group chunk
+  // 2 wave + (q >> 1) of rows 4g + e (+16 for the second half).
+  const int e = l16 >> 2, qq = l16 & 3;
+  const int brow = 4 * g + e;
+  const int b_off = brow * 128 + 16 * ((2 * wave + (qq >> 1)) ^ swz(brow)) + 8 * (qq & 1);
+  // Copies: wave w moves rows 8w .. 8w+7 of every chunk group; lane l -> row 8w + l/8, physical
+  // chunk l%8 = logical chunk (l%8) ^ swz(row).
+  const int crow = 8 * wave + (lane >> 3);
+  const int cchunk = (lane & 7) ^ swz(crow & 15);
+
+  bool first_segment = true;
+  for (int ph = 0; ph < 2; ++ph) {
+    const int g_lo = ph == 0 ? lo : max(lo, pp.steps_a);
+    const int g_hi = ph == 0 ? min(hi, pp.steps_a) : hi;
+    if (g_lo >= g_hi) continue;
+    const int count = g_hi - g_lo;
+    const int kb = ph == 0 ? pp.kb_a : pp.kb_b;
+    const int dir = ph == 0 ? -1 : 1;
+    const int rt_first = ph == 0 ? p.n_rt - 1 - g_lo
+                                 : first_row_tile(p.causal, p.Sq, p.Sk, p.H, kb) + (g_lo - pp.steps_a);
+    if (!first_segment) __syncthreads();   // the previous segment's last tile is still being read
+    first_segment = false;
+    const int key0 = kb * kKeys;
+
+    // K_lat rows of this wave's two key blocks, B operand of S = Q K^T (zero past Sk):
+    // kreg[kk][c] = K[key0 + 32 kp + 16 kk + l16][32 c + 8 g .. +7]
+    bf16x8 kreg[2][18];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int key = key0 + 32 * kp + 16 * kk + l16;
+      const bool kvalid = key < p.Sk;
+      const bf16* krow = p.k + b * p.k_sb + (int64_t)(kvalid ? key : 0) * p.k_ss + 8 * g;
+#pragma unroll
+      for (int c = 0; c < 18; ++c) {
+        const bf16x8 v = *reinterpret_cast<const bf16x8*>(krow + 32 * c);
+        kreg[kk][c] = kvalid ? v : bf16x8{};
+      }
+    }
+
+    f32x4 acc[4][9];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int v = 0; v < 9; ++v) acc[a][v] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Stage row tile rt into LDS stage st (rows past R re-read row R-1: finite, and masked by
+    // their +inf lse2).
+    auto stage = [&](int rt, int st) {
+      const int r = min(rt * kRows + crow, p.R - 1);
+      const int pos = r / p.H, h = r - pos * p.H;
+      const char* qsrc = reinterpret_cast<const char*>(p.q + b * p.q_sb + h * p.q_sh + pos * p.q_ss + 8 * cchunk);
+      const char* osrc = reinterpret_cast<const char*>(p.dout + b * p.do_sb + h * p.do_sh + pos * p.do_ss + 8 * cchunk);
+      const unsigned dst = lds_base + st * kStageBytes + wave * 1024;
+#pragma unroll
+      for (int gq = 0; gq < kQGroups; ++gq) dma16_addr(qsrc + 128 * gq, dst + gq * kGroupBytes);
+#pragma unroll
+      for (int go = 0; go < kOGroups; ++go) dma16_addr(osrc + 128 * go, dst + kQBytes + go * kGroupBytes);
+    };
+    // (lse2, D) and key limit of this lane's 4 S-phase rows 32 rt + 16 rb + 4 g + i.
+    float lse2[4], dval[4];
+    int lim[4];
+    auto row_stats = [&](int rt, float (&ls)[4], float (&dv)[4], int (&lm)[4]) {
+      const int r0 = rt * kRows + 16 * rb + 4 * g;
+      const float4* src = reinterpret_cast<const float4*>(p.lsed + (int64_t)b * p.n_rt * kRows + r0);
+      const float4 a0 = src[0], a1 = src[1];
+      ls[0] = a0.x; dv[0] = a0.y; ls[1] = a0.z; dv[1] = a0.w;
+      ls[2] = a1.x; dv[2] = a1.y; ls[3] = a1.z; dv[3] = a1.w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = r0 + i;
+        const int pos = r / p.H;
+        lm[i] = r >= p.R ? -1 : (p.causal ? min(pos + off, p.Sk - 1) : p.Sk - 1);
+      }
+    };
+
+    stage(rt_first, 0);
+    row_stats(rt_first, lse2, dval, lim);
+    for (int s = 0; s < count; ++s) {
+      const int rt = rt_first + dir * s;
+      const int st = s & 1;
+      wait_vmem();
+      __syncthreads();   // tile s landed everywhere; the other stage and the exchange are free
+      float lse2n[4], dvaln[4];
+      int limn[4];
+      if (s + 1 < count) {
+        stage(rt + dir, st ^ 1);
+        row_stats(rt + dir, lse2n, dvaln, limn);
+      }
+      const DMLA_LDS char* qt = lds + st * kStageBytes;
+      const DMLA_LDS char* ot = qt + kQBytes;
+
+      // ---- S-phase ----
+      f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+      f32x4 pacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int c = 0; c < 18; ++c) {
+        const bf16x8 a = lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(
+            qt + (c >> 1) * kGroupBytes + ((c & 1) ? a_off1 : a_off0)));
+        sacc[0] = mfma_bf16(a, kreg[0][c], sacc[0]);
+        sacc[1] = mfma_bf16(a, kreg[1][c], sacc[1]);
+      }
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const bf16x8 a = lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(
+            ot + (c >> 1) * kGroupBytes + ((c & 1) ? a_off1 : a_off0)));
+        pacc[0] = mfma_bf16(a, kreg[0][c], pacc[0]);
+        pacc[1] = mfma_bf16(a, kreg[1][c], pacc[1]);
+      }
+      // P and dS' for keys key0 + 32 kp + 16 kk + l16, rows 16 rb + 4 g + i of the tile.
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int key = key0 + 32 * kp + 16 * kk + l16;
+        float pv[4], dsv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pr = key <= lim[i] ? fast_exp2(sacc[kk][i] * scale_log2 - lse2[i]) : 0.f;
+          pv[i] = pr;
+          dsv[i] = scale * pr * (pacc[kk][i] - dval[i]);
+        }
+        const f16x4 pb = to_f16x4(pv[0], pv[1], pv[2], pv[3]);
+        const f16x4 db = to_f16x4(dsv[0], dsv[1], dsv[2], dsv[3]);
+        const int kbl = 2 * kp + kk;
+        *reinterpret_cast<DMLA_LDS f16x4*>(xbuf + kbl * 1024 + lane * 16 + 8 * rb) = pb;
+        *reinterpret_cast<DMLA_LDS f16x4*>(xbuf + 4096 + kbl * 1024 + lane * 16 + 8 * rb) = db;
+        _Float16* dsblk = p.ds + ((((int64_t)b * 2 * p.n_rt + 2 * rt + rb) * (4 * p.n_kb)) + 4 * kb + kbl) * 256;
+        *reinterpret_cast<f16x4*>(dsblk + 4 * lane) = db;
+      }
+      __syncthreads();   // exchange written
+
+      // ---- dK-phase ----
+      f16x8 pT[4], dsT[4];
+#pragma unroll
+      for (int kbl = 0; kbl < 4; ++kbl) {
+        pT[kbl] = *reinterpret_cast<const DMLA_LDS f16x8*>(xbuf + kbl * 1024 + lane * 16);
+        dsT[kbl] = *reinterpret_cast<const DMLA_LDS f16x8*>(xbuf + 4096 + kbl * 1024 + lane * 16);
+      }
+#pragma unroll
+      for (int v = 0; v < 9; ++v) {
+        const DMLA_LDS char* qc = qt + v * kGroupBytes + b_off;
+        const f16x8 qb = bf16_to_f16(lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(qc)),
+                                     lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(qc + 16 * 128)));
+#pragma unroll
+        for (int kbl = 0; kbl < 4; ++kbl) acc[kbl][v] = mfma_f16(dsT[kbl], qb, acc[kbl][v]);
+        if (v < 8) {
+          const DMLA_LDS char* oc = ot + v * kGroupBytes + b_off;
+          const f16x8 ob = bf16_to_f16(lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(oc)),
+                                       lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(oc + 16 * 128)));
+#pragma unroll
+          for (int kbl = 0; kbl < 4; ++kbl) acc[kbl][v] = mfma_f16(pT[kbl], ob, acc[kbl][v]);
+        }
+      }
+      if (s + 1 < count) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lse2[i] = lse2n[i];
+          dval[i] = dvaln[i];
+          lim[i] = limn[i];
+        }
+      }
+    }
+
+    // Partial of this segment: acc[kbl][v] holds dK[16 kbl + 4 g + i][16 (wave + 4 v) + l16].
+    float* dst = p.part + ((int64_t)u * 2 + ph) * kPartFloats;
+#pragma unroll
+    for (int kbl = 0; kbl < 4; ++kbl)
+#pragma unroll
+      for (int v = 0; v < 9; ++v)
+        *reinterpret_cast<f32x4*>(dst + ((kbl * kCb + wave + 4 * v) * 64 + lane) * 4) = acc[kbl][v];
+  }
+}
+
+// ---- 4. dQ = dS' K_lat ----------------------------------------------------------------------
+// Workgroup = 4 waves on 64 rows x 576 dims; wave w owns column blocks w, w+4, .., w+32 of all
+// four row blocks (36 accumulators).  Per 32-key tile: dS' (A operand, row fixed per lane) from
+// the stored C-order blocks through ds_read_b64_tr_b16, K^T (B operand) with b128 reads.
+__global__ void __launch_bounds__(kBwdThreads, 1) bwd_dq_kernel(BwdParams p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kDqLds];
+  DMLA_LDS char* lds = (DMLA_LDS char*)smem;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int lane = lane_id();
+  const int n_t = (p.R + 63) / 64;
+  // Heaviest (latest) row tiles first.
+  const int b = (int)blockIdx.x % p.B;
+  const int t = n_t - 1 - (int)blockIdx.x / p.B;
+  const int row0 = 64 * t;
+  const int last_row = min(p.R, row0 + 64) - 1;
+  const int kmax = p.causal ? min(p.Sk - 1, last_row / p.H + (p.Sk - p.Sq)) : p.Sk - 1;
+  const int n_kt = kmax >= 0 ? kmax / 32 + 1 : 0;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int e = l16 >> 2, qq = l16 & 3;
+  const unsigned lds_base = lds_addr(lds);
+
+  // Copies.  dS': wave w moves row block 4t + w, key blocks 2 kt, 2 kt + 1 (1 KB contiguous).
+  // K^T: 16 dims x 32 keys per copy (1 KB), wave w copies dim blocks w, w+4, .. (9 copies);
+  // lane l -> dim 16 n + l/4, physical chunk l%4 = logical chunk (l%4) ^ (l/16).
+  const unsigned kt_voff = (unsigned)(((lane >> 2) * p.kt_ld + 8 * ((lane & 3) ^ (lane >> 4))) * 2);
+  auto stage = [&](int kt, int st) {
+    const unsigned dst = lds_base + st * kDqStageBytes;
+    const _Float16* dsrc = p.ds + ((((int64_t)b * 2 * p.n_rt + 4 * t + wave) * (4 * p.n_kb)) + 2 * kt) * 256;
+    dma16(dsrc, 16u * lane, dst + wave * 1024);
+#pragma unroll
+    for (int m = 0; m < 9; ++m) {
+      const int n = wave + 4 * m;
+      const _Float16* ksrc = p.kt + ((int64_t)b * kDqk + 16 * n) * p.kt_ld + 32 * kt;
+      dma16(ksrc, kt_voff, dst + kDqDsBytes + n * 1024);
+    }
+  };
+  // dS' A operand of row block rq, half h: lane 4e+q of group g reads C-order lane
+  // 16 q + 8 (g & 1) + 4 h + e of key block g >> 1 (see the tr-read rule in dmla_common.h).
+  const int a_off = (g >> 1) * 512 + 8 * (16 * qq + 8 * (g & 1) + e);
+  // K^T B operand of column block wave + 4u: dim row 16 cb + l16, logical chunk g.
+  const int b_off = kDqDsBytes + wave * 1024 + l16 * 64 + 16 * (g ^ e);
+
+  f32x4 acc[4][9];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int v = 0; v < 9; ++v) acc[a][v] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (n_kt > 0) stage(0, 0);
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int st = kt & 1;
+    wait_vmem();
+    __syncthreads();
+    if (kt + 1 < n_kt) stage(kt + 1, st ^ 1);
+    const DMLA_LDS char* sb = lds + st * kDqStageBytes;
+    f16x8 a[4];
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const DMLA_LDS char* ab = sb + rq * 1024 + a_off;
+      const f16x4 lo = lds_read_tr16_f16(reinterpret_cast<const DMLA_LDS f16x4*>(ab));
+      const f16x4 hi = lds_read_tr16_f16(reinterpret_cast<const DMLA_LDS f16x4*>(ab + 32));
+      a[rq] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+#pragma unroll
+    for (int v = 0; v < 9; ++v) {
+      const f16x8 kb = *reinterpret_cast<const DMLA_LDS f16x8*>(sb + b_off + v * 4096);
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) acc[rq][v] = mfma_f16(a[rq], kb, acc[rq][v]);
+    }
+  }
+
+  // acc[rq][v] holds dQ[row0 + 16 rq + 4 g + i][16 (wave + 4 v) + l16].
+#pragma unroll
+  for (int rq = 0; rq < 4; ++rq) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = row0 + 16 * rq + 4 * g + i;
+      if (r >= p.R) continue;
+      const int pos = r / p.H, h = r - pos * p.H;
+      const int64_t base = b * p.dq_sb + h * p.dq_sh + pos * p.dq_ss + l16;
+#pragma unroll
+      for (int v = 0; v < 9; ++v) {
+        const int col = 16 * (wave + 4 * v);
+        if (p.dq_fp32) static_cast<float*>(p.dq)[base + col] = acc[rq][v][i];
+        else static_cast<bf16*>(p.dq)[base + col] = (bf16)acc[rq][v][i];
+      }
+    }
+  }
+}
+
+// ---- 5. dK_lat = sum of the segment partials ------------------------------------------------
+// One workgroup per (batch, 64-key block, 16-key block); the segments of the block are added in
+// part order, so the result does not depend on scheduling.
+__global__ void __launch_bounds__(256) bwd_dk_reduce_kernel(BwdParams p) {
+  const int b = blockIdx.z, kb = blockIdx.y, kbl = blockIdx.x;
+  const int pi = min(kb, p.n_kb - 1 - kb);
+  const int ph = kb == pi ? 0 : 1;
+  const PairPlan pp = pair_plan(p.causal, p.Sq, p.Sk, p.H, p.n_rt, p.n_kb, pi);
+  const int iv_lo = ph == 0 ? 0 : pp.steps_a;
+  const int iv_hi = ph == 0 ? pp.steps_a : pp.total;
+  for (int idx = threadIdx.x; idx < kCb * 64; idx += 256) {
+    const int cb = idx >> 6, ln = idx & 63;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < p.parts; ++j) {
+      const int lo = part_begin(pp.total, p.parts, j), hi = part_begin(pp.total, p.parts, j + 1);
+      if (max(lo, iv_lo) >= min(hi, iv_hi)) continue;
+      const int u = (b * p.parts + j) * p.n_pairs + pi;
+      s += *reinterpret_cast<const f32x4*>(p.part + ((int64_t)u * 2 + ph) * kPartFloats +
+                                           ((kbl * kCb + cb) * 64 + ln) * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = kb * kKeys + 16 * kbl + 4 * (ln >> 4) + i;
+      if (key >= p.Sk) continue;
+      const int64_t o = b * p.dk_sb + key * p.dk_ss + 16 * cb + (ln & 15);
+      if (p.dk_fp32) static_cast<float*>(p.dk)[o] = s[i];
+      else static_cast<bf16*>(p.dk)[o] = (bf16)s[i];
+    }
+  }
+}
+
+// ---- host-side planning ----------------------------------------------------------------------
+struct BwdPlan {
+  int R, n_rt, n_kb, n_pairs, parts, n_items, kt_ld;
+  int64_t off_lsed, off_kt, off_ds, off_part, bytes;
+};
+
+int64_t round256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+BwdPlan make_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int causal, int cus) {
+  BwdPlan pl = {};
+  pl.R = (int)(H * Sq);
+  pl.n_rt = 2 * (int)((pl.R + 63) / 64);
+  pl.n_kb = (int)((Sk + kKeys - 1) / kKeys);
+  pl.n_pairs = (pl.n_kb + 1) / 2;
+  int max_total = 1;
+  for (int i = 0; i < pl.n_pairs; ++i)
+    max_total = max(max_total, pair_plan(causal, (int)Sq, (int)Sk, (int)H, pl.n_rt, pl.n_kb, i).total);
+  const int64_t base = B * pl.n_pairs;
+  int parts = (int)((cus + base - 1) / base);
+  parts = max(1, min(parts, min(kMaxParts, max_total)));
+  pl.parts = parts;
+  pl.n_items = (int)(base * parts);
+  pl.kt_ld = kKeys * pl.n_kb;
+  int64_t o = 0;
+  pl.off_lsed = o; o += round256(B * pl.n_rt * kRows * 8);
+  pl.off_kt = o;   o += round256(B * kDqk * (int64_t)pl.kt_ld * 2);
+  pl.off_ds = o;   o += round256(B * 2 * (int64_t)pl.n_rt * 4 * pl.n_kb * 512);
+  pl.off_part = o; o += round256((int64_t)pl.n_items * 2 * kPartFloats * 4);
+  pl.bytes = o;
+  return pl;
+}
+
+}  // namespace
+}  // namespace dmla
+
+using namespace dmla;
+
+extern "C" int64_t dmla_bwd_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t d_qk,
+                                            int64_t d_v, int causal) {
+  if (B <= 0 || H <= 0 || Sq <= 0 || Sk <= 0 || d_qk != kDqk || d_v != kDv) return 0;
+  if (H * Sq > ((int64_t)1 << 30) || Sk > ((int64_t)1 << 30)) return 0;
+  return make_plan(B, H, Sq, Sk, causal ? 1 : 0, device_cu_count()).bytes;
+}
+
+extern "C" int dmla_bwd_cache_latent(const void* q, const void* k_lat, const void* o, const void* dout,
+                                     const float* m, const float* l, void* dq, void* dk_lat, int64_t B,
+                                     int64_t H, int64_t Sq, int64_t Sk, int64_t d_qk, int64_t d_v,
+                                     int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t k_sb, int64_t k_ss,
+                                     int64_t o_sb, int64_t o_sh, int64_t o_ss, int64_t do_sb,
+                                     int64_t do_sh, int64_t do_ss, int64_t dq_sb, int64_t dq_sh,
+                                     int64_t dq_ss, int64_t dk_sb, int64_t dk_ss, int dq_fp32,
+                                     int dk_fp32, float softmax_scale, int causal, void* workspace,
+                                     int64_t workspace_bytes, dmla_stream_t stream) {
+  clear_error();
+  if (!q || !k_lat || !o || !dout || !m || !l || !dq || !dk_lat)
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_bwd_cache_latent: null pointer argument");
+  if (B < 0 || H < 0 || Sq < 0 || Sk < 0)
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_bwd_cache_latent: negative size");
+  if (d_qk != kDqk || d_v != kDv)
+    return fail(DMLA_ERR_UNSUPPORTED, "dmla_bwd_cache_latent: only d_qk=576, d_v=512 is compiled (got %lld, %lld)",
+                (long long)d_qk, (long long)d_v);
+  if (!(softmax_scale > 0.f) || !__builtin_isfinite(softmax_scale))
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_bwd_cache_latent: softmax_scale must be finite and > 0");
+  if (!aligned16(q) || !aligned16(k_lat) || !aligned16(o) || !aligned16(dout) || !aligned16(m) ||
+      !aligned16(l) || !aligned16(dq) || !aligned16(dk_lat))
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_bwd_cache_latent: tensors must be 16-byte aligned");
+  if (!mult8(q_sb) || !mult8(q_sh) || !mult8(q_ss) || !mult8(k_sb) || !mult8(k_ss) || !mult8(o_sb) ||
+      !mult8(o_sh) || !mult8(o_ss) || !mult8(do_sb) || !mult8(do_sh) || !mult8(do_ss))
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_bwd_cache_latent: input strides must be multiples of 8 elements");
+  if (H * Sq > ((int64_t)1 << 30) || Sk > ((int64_t)1 << 30))
+    return fail(DMLA_ERR_UNSUPPORTED, "dmla_bwd_cache_latent: size too large");
+  if (B == 0 || H == 0 || Sq == 0) return DMLA_OK;
+  if (Sk == 0) return fail(DMLA_ERR_INVALID_ARG, "dmla_bwd_cache_latent: Sk must be > 0");
+
+  const BwdPlan pl = make_plan(B, H, Sq, Sk, causal ? 1 : 0, device_cu_count());
+  if (workspace_bytes < pl.bytes || (!workspace && pl.bytes > 0))
+    return fail(DMLA_ERR_WORKSPACE, "dmla_bwd_cache_latent: workspace of %lld bytes needed, got %lld",
+                (long long)pl.bytes, (long long)workspace_bytes);
+  if (!aligned16(workspace))
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_bwd_cache_latent: workspace must be 16-byte aligned");
+
+  BwdParams p = {};
+  p.q = static_cast<const bf16*>(q);
+  p.k = static_cast<const bf16*>(k_lat);
+  p.o = static_cast<const bf16*>(o);
+  p.dout = static_cast<const bf16*>(dout);
+  p.m = m;
+  p.l = l;
+  p.dq = dq;
+  p.dk = dk_lat;
+  p.dq_fp32 = dq_fp32 ? 1 : 0;
+  p.dk_fp32 = dk_fp32 ? 1 : 0;
+  p.q_sb = q_sb; p.q_sh = q_sh; p.q_ss = q_ss;
+  p.k_sb = k_sb; p.k_ss = k_ss;
+  p.o_sb = o_sb; p.o_sh = o_sh; p.o_ss = o_ss;
+  p.do_sb = do_sb; p.do_sh = do_sh; p.do_ss = do_ss;
+  p.dq_sb = dq_sb; p.dq_sh = dq_sh; p.dq_ss = dq_ss;
+  p.dk_sb = dk_sb; p.dk_ss = dk_ss;
+  p.B = (int)B; p.H = (int)H; p.Sq = (int)Sq; p.Sk = (int)Sk;
+  p.causal = causal ? 1 : 0;
+  p.scale = softmax_scale;
+  p.scale_log2 = softmax_scale * kLog2e;
+  p.R = pl.R; p.n_rt = pl.n_rt; p.n_kb = pl.n_kb; p.n_pairs = pl.n_pairs; p.parts = pl.parts;
+  p.n_items = pl.n_items; p.kt_ld = pl.kt_ld;
+  char* ws = static_cast<char*>(workspace);
+  p.lsed = reinterpret_cast<float2*>(ws + pl.off_lsed);
+  p.kt = reinterpret_cast<_Float16*>(ws + pl.off_kt);
+  p.ds = reinterpret_cast<_Float16*>(ws + pl.off_ds);
+  p.part = reinterpret_cast<float*>(ws + pl.off_part);
+
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)pl.n_rt, (unsigned)B), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(bwd_kt_kernel, dim3(kDqk / 64, (unsigned)pl.n_kb, (unsigned)B), dim3(256), 0, s, p);
+  const int64_t grid_kv = 8 * ((pl.n_items + 7) / 8);
+  hipLaunchKernelGGL(bwd_dkdv_kernel, dim3((unsigned)grid_kv), dim3(kBwdThreads), 0, s, p);
+  const int64_t grid_q = B * ((pl.R + 63) / 64);
+  if (grid_q > 0x7fffffff) return fail(DMLA_ERR_UNSUPPORTED, "dmla_bwd_cache_latent: grid too large");
+  hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)grid_q), dim3(kBwdThreads), 0, s, p);
+  hipLaunchKernelGGL(bwd_dk_reduce_kernel, dim3(4, (unsigned)pl.n_kb, (unsigned)B), dim3(256), 0, s, p);
+  return check_launch("dmla_bwd_cache_latent");
+}

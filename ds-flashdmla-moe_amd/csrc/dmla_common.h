@@ -19,6 +19,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 #define DMLA_LDS __attribute__((address_space(3)))
 
@@ -28,6 +30,27 @@ constexpr float kNegInf = -__builtin_inff();
 
 __device__ __forceinline__ f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Same tile shapes and lane layouts as the bf16 form.
+__device__ __forceinline__ f32x4 mfma_f16(const f16x8& a, const f16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// bf16 -> fp16 of 8 values.  Exact for |x| in fp16's normal range: bf16's 8-bit significand
+// fits fp16's 11 bits, so the round-toward-zero pack never rounds; larger magnitudes saturate
+// at +-65504 and values below 2^-14 lose low bits as fp16 subnormals.
+__device__ __forceinline__ f16x8 bf16_to_f16(const bf16x4& lo, const bf16x4& hi) {
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
+  const auto p0 = __builtin_amdgcn_cvt_pkrtz(__uint_as_float(a[0] << 16), __uint_as_float(a[0] & 0xffff0000u));
+  const auto p1 = __builtin_amdgcn_cvt_pkrtz(__uint_as_float(a[1] << 16), __uint_as_float(a[1] & 0xffff0000u));
+  const auto p2 = __builtin_amdgcn_cvt_pkrtz(__uint_as_float(b[0] << 16), __uint_as_float(b[0] & 0xffff0000u));
+  const auto p3 = __builtin_amdgcn_cvt_pkrtz(__uint_as_float(b[1] << 16), __uint_as_float(b[1] & 0xffff0000u));
+  f16x8 r;
+  r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+  r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+  return r;
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -56,6 +79,12 @@ __device__ __forceinline__ void dma16(const void* sbase, unsigned voff, unsigned
                : "s"(sl), "v"(voff), "s"(reinterpret_cast<const void*>(sb))
                : "memory", "m0");
 }
+// Same copy with a full 64-bit global address per lane (rows of one tile that are far apart,
+// e.g. query rows of different heads).
+__device__ __forceinline__ void dma16_addr(const void* gaddr, unsigned lds_addr) {
+  const unsigned sl = __builtin_amdgcn_readfirstlane(lds_addr);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(sl), "v"(gaddr) : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 __device__ __forceinline__ unsigned lds_addr(const DMLA_LDS void* p) {
@@ -64,6 +93,11 @@ __device__ __forceinline__ unsigned lds_addr(const DMLA_LDS void* p) {
 
 __device__ __forceinline__ bf16x4 lds_read_tr16(const DMLA_LDS bf16x4* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(const_cast<DMLA_LDS bf16x4*>(p));
+}
+
+__device__ __forceinline__ f16x4 lds_read_tr16_f16(const DMLA_LDS f16x4* p) {
+  typedef __fp16 fp16v4 __attribute__((__vector_size__(8)));  // the builtin's own operand type
+  return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((DMLA_LDS fp16v4*)p));
 }
 
 __device__ __forceinline__ bf16x8 lds_read_b128(const DMLA_LDS bf16x8* p) { return *p; }

@@ -60,6 +60,14 @@ SIGNATURES = {
         + [_i64] * 7  # q_sb q_sh kv_sp kv_ss bt_sb o_sb o_sh
         + [_f32, _ptr, _i64, _ptr],  # scale, workspace, workspace_bytes, stream
     ),
+    "dmla_bwd_workspace_bytes": (_i64, [_i64] * 6 + [_int]),  # B H Sq Sk d_qk d_v causal
+    "dmla_bwd_cache_latent": (
+        _int,
+        [_ptr] * 8  # q, k_lat, o, dout, m, l, dq, dk_lat
+        + [_i64] * 6  # B, H, Sq, Sk, d_qk, d_v
+        + [_i64] * 16  # q(3) k(2) o(3) dout(3) dq(3) dk(2) strides
+        + [_int, _int, _f32, _int, _ptr, _i64, _ptr],  # dq_fp32 dk_fp32 scale causal ws ws_bytes stream
+    ),
 }
 
 _lib = None

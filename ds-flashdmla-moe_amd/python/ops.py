@@ -166,13 +166,69 @@ class FlashDMLACacheLatent(torch.autograd.Function):
     @staticmethod
     def backward(ctx, do):
         q, k_lat, o, m, l = ctx.saved_tensors
-        dq, dk_lat = flash_dmla_bwd(q, k_lat, o, do, m, l, ctx.d_v, ctx.softmax_scale, ctx.causal)
-        return dq, dk_lat, None, None, None
+        dq, dk_lat = flash_dmla_bwd(q, k_lat, o, do.to(torch.bfloat16).contiguous(), m, l, ctx.d_v,
+                                    ctx.softmax_scale, ctx.causal)
+        return dq, dk_lat.to(k_lat.dtype), None, None, None
 
 
-def flash_dmla_bwd(q, k_lat, o, do, m, l, d_v=D_V, softmax_scale=None, causal=True):
-    """Cache-latent DMLA backward from the saved statistics: returns (dq, dk_lat)."""
-    raise NotImplementedError("flash_dmla_bwd: the backward kernel is not built into this library yet")
+def flash_dmla_bwd(
+    q: torch.Tensor,
+    k_lat: torch.Tensor,
+    o: torch.Tensor,
+    do: torch.Tensor,
+    m: torch.Tensor,
+    l: torch.Tensor,
+    d_v: int = D_V,
+    softmax_scale: Optional[float] = None,
+    causal: bool = True,
+    dq_dtype: Optional[torch.dtype] = None,
+    dk_dtype: torch.dtype = torch.float32,
+    check_range: bool = False,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Cache-latent DMLA backward from the saved statistics: returns (dq, dk_lat).
+
+    dq [B, H, Sq, 576] (dq_dtype, default q.dtype) and dk_lat [B, Sk, 576] (dk_dtype, default
+    float32: dk_lat sums P^T dO and dS^T q over every head and position, so its large entries
+    would lose more to a bf16 rounding than the accumulation itself does).  dk_lat already holds
+    the V_lat gradient in its first d_v columns.  m, l must be the forward's statistics.
+    The second-stage products (dS^T q, P^T dO, dS K) run on fp16 operands, with q, dO and
+    k_lat converted exactly; check_range=True verifies on the host (one device sync) that they
+    stay inside fp16's range instead of saturating.
+    """
+    _check_bf16("q", q, 4)
+    _check_bf16("k_lat", k_lat, 3)
+    _check_bf16("o", o, 4)
+    _check_bf16("do", do, 4)
+    B, H, Sq, Dqk = q.shape
+    Sk = k_lat.shape[1]
+    _require(k_lat.shape[0] == B and k_lat.shape[2] == Dqk, "k_lat shape does not match q")
+    _require(tuple(o.shape) == (B, H, Sq, d_v), f"o must be [B, H, Sq, {d_v}]")
+    _require(tuple(do.shape) == (B, H, Sq, d_v), f"do must be [B, H, Sq, {d_v}]")
+    for name, t in (("m", m), ("l", l)):
+        _require(t.dtype == torch.float32 and t.is_cuda and t.is_contiguous() and tuple(t.shape) == (B, H, Sq),
+                 f"{name} must be a contiguous float32 GPU tensor [B, H, Sq]")
+    if check_range:
+        for name, t in (("q", q), ("k_lat", k_lat), ("do", do)):
+            _require(bool(torch.isfinite(t).all()) and float(t.abs().max()) <= 65504.0,
+                     f"{name} has entries outside fp16's finite range (|x| <= 65504)")
+    dq_dtype = q.dtype if dq_dtype is None else dq_dtype
+    _require(dq_dtype in (torch.bfloat16, torch.float32) and dk_dtype in (torch.bfloat16, torch.float32),
+             "gradient dtypes must be bfloat16 or float32")
+    dq = torch.empty((B, H, Sq, Dqk), dtype=dq_dtype, device=q.device)
+    dk = torch.empty((B, Sk, Dqk), dtype=dk_dtype, device=q.device)
+    ws_bytes = int(_lib.lib().dmla_bwd_workspace_bytes(B, H, Sq, Sk, Dqk, d_v, 1 if causal else 0))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
+    _lib.call(
+        "dmla_bwd_cache_latent",
+        _ptr(q), _ptr(k_lat), _ptr(o), _ptr(do), _ptr(m), _ptr(l), _ptr(dq), _ptr(dk),
+        B, H, Sq, Sk, Dqk, d_v,
+        q.stride(0), q.stride(1), q.stride(2), k_lat.stride(0), k_lat.stride(1),
+        o.stride(0), o.stride(1), o.stride(2), do.stride(0), do.stride(1), do.stride(2),
+        dq.stride(0), dq.stride(1), dq.stride(2), dk.stride(0), dk.stride(1),
+        1 if dq_dtype == torch.float32 else 0, 1 if dk_dtype == torch.float32 else 0,
+        _scale(softmax_scale, Dqk), 1 if causal else 0, _ptr(ws), ws_bytes, _stream(q),
+    )
+    return dq, dk
 
 
 def flash_dmla(q, k_lat, d_v=D_V, softmax_scale=None, causal=True):

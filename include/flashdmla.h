@@ -94,6 +94,42 @@ int dmla_decode_paged(const void* q, const void* kv_pool, const int32_t* block_t
                       float softmax_scale, void* workspace, int64_t workspace_bytes,
                       dmla_stream_t stream);
 
+/*
+ * Cache-latent DMLA backward from the forward's saved statistics.
+ * Replaces: fa2_backward (csrc/attention/fa2_bwd.cu:319-356, math of :198-310) specialised
+ * to the cache-latent mode of README.md:12,15 -- the role of the absent
+ * csrc/attention/fa2_dmla_bwd.cu (README.md:46).
+ *
+ *   q, k_lat, o    as for dmla_fwd_cache_latent (o is the forward's output)
+ *   dout   [B, H, Sq, d_v]  bf16  strides (do_sb, do_sh, do_ss)
+ *   m, l   [B, H, Sq]       fp32  contiguous, exactly as dmla_fwd_cache_latent wrote them
+ *   dq     [B, H, Sq, d_qk] bf16, or fp32 when dq_fp32 != 0; strides (dq_sb, dq_sh, dq_ss)
+ *   dk_lat [B, Sk, d_qk]    bf16, or fp32 when dk_fp32 != 0; strides (dk_sb, dk_ss)
+ *
+ *   P = exp(s - m) / l, D_i = sum_d dout_i * o_i, dP = dout V^T, dS = P * (dP - D),
+ *   dq = scale dS K_lat, dk_lat = scale sum_h dS^T q + [sum_h P^T dout, 0]  (the V_lat
+ *   gradient folded into the first d_v columns).  Rows with l = 0 contribute nothing.
+ *   S = q K^T and dP = dout V^T use the bf16 inputs as they are; dS^T q, P^T dout and dS K
+ *   take fp16 operands (P and dS rounded to fp16; q, dout, K converted to fp16, exact for
+ *   magnitudes in fp16's normal range, saturating above 65504).  All products accumulate in
+ *   fp32.
+ *   The result is deterministic (no atomics).  workspace: device memory of at least
+ *   dmla_bwd_workspace_bytes(...) bytes for the same sizes on the current device, 16-byte
+ *   aligned; its contents on entry do not matter.
+ * Supported: d_qk = 576, d_v = 512.
+ */
+int64_t dmla_bwd_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t d_qk,
+                                 int64_t d_v, int causal);
+int dmla_bwd_cache_latent(const void* q, const void* k_lat, const void* o, const void* dout,
+                          const float* m, const float* l, void* dq, void* dk_lat, int64_t B,
+                          int64_t H, int64_t Sq, int64_t Sk, int64_t d_qk, int64_t d_v,
+                          int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t k_sb, int64_t k_ss,
+                          int64_t o_sb, int64_t o_sh, int64_t o_ss, int64_t do_sb, int64_t do_sh,
+                          int64_t do_ss, int64_t dq_sb, int64_t dq_sh, int64_t dq_ss,
+                          int64_t dk_sb, int64_t dk_ss, int dq_fp32, int dk_fp32,
+                          float softmax_scale, int causal, void* workspace,
+                          int64_t workspace_bytes, dmla_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

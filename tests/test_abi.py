@@ -98,3 +98,48 @@ def test_python_wrappers_reject_cpu_tensors_and_bad_shapes():
 def test_error_message_is_raised_as_exception():
     with pytest.raises(_lib.DmlaUnsupported, match="576"):
         _lib.check("dmla_fwd_cache_latent", _fwd(dqk=64, dv=32))
+
+
+def _bwd(ws_bytes=None, **kw):
+    args = dict(q=1 << 20, k=1 << 20, o=1 << 20, do=1 << 20, m=1 << 20, l=1 << 20, dq=1 << 20, dk=1 << 20,
+                B=1, H=16, Sq=64, Sk=64, dqk=576, dv=512, scale=0.07, causal=1, ws=1 << 20)
+    args.update(kw)
+    P = ctypes.c_void_p
+    lib = _lib.lib()
+    need = lib.dmla_bwd_workspace_bytes(args["B"], args["H"], args["Sq"], args["Sk"], args["dqk"], args["dv"],
+                                        args["causal"])
+    return lib.dmla_bwd_cache_latent(
+        P(args["q"]), P(args["k"]), P(args["o"]), P(args["do"]), P(args["m"]), P(args["l"]), P(args["dq"]),
+        P(args["dk"]), args["B"], args["H"], args["Sq"], args["Sk"], args["dqk"], args["dv"],
+        16 * 64 * 576, 64 * 576, 576, 64 * 576, 576, 16 * 64 * 512, 64 * 512, 512, 16 * 64 * 512, 64 * 512, 512,
+        16 * 64 * 576, 64 * 576, 576, 64 * 576, 576, 0, 1, args["scale"], args["causal"], P(args["ws"]),
+        need - 256 if ws_bytes is None else ws_bytes, None)
+
+
+def test_bwd_workspace_query_and_argument_errors():
+    lib = _lib.lib()
+    need = lib.dmla_bwd_workspace_bytes(1, 16, 64, 64, 576, 512, 1)
+    assert need > 0 and need % 256 == 0
+    assert lib.dmla_bwd_workspace_bytes(1, 16, 64, 64, 64, 32, 1) == 0       # unsupported dims
+    assert lib.dmla_bwd_workspace_bytes(0, 16, 64, 64, 576, 512, 1) == 0     # empty problem
+    # The workspace holds the dS' blocks of every (16-row, 16-key) pair: at least 2 bytes per
+    # (row, key) of the problem.
+    assert lib.dmla_bwd_workspace_bytes(1, 16, 512, 512, 576, 512, 1) >= 2 * 16 * 512 * 512
+    assert _bwd() == _lib.DMLA_ERR_WORKSPACE                                 # 256 bytes short
+    assert b"workspace" in lib.dmla_last_error()
+    assert _bwd(q=None) == _lib.DMLA_ERR_INVALID_ARG
+    assert _bwd(m=(1 << 20) + 4) == _lib.DMLA_ERR_INVALID_ARG                # misaligned m
+    assert _bwd(dqk=64, dv=32) == _lib.DMLA_ERR_UNSUPPORTED
+    assert _bwd(scale=0.0) == _lib.DMLA_ERR_INVALID_ARG
+    assert _bwd(Sk=0, ws_bytes=0) == _lib.DMLA_ERR_INVALID_ARG
+    assert _bwd(B=0, ws_bytes=0) == _lib.DMLA_OK                             # empty: nothing launched
+    assert lib.dmla_last_error() == b""
+
+
+def test_bwd_python_wrapper_rejects_cpu_tensors():
+    q = torch.zeros(1, 2, 4, 576, dtype=torch.bfloat16)
+    k = torch.zeros(1, 4, 576, dtype=torch.bfloat16)
+    o = torch.zeros(1, 2, 4, 512, dtype=torch.bfloat16)
+    m = torch.zeros(1, 2, 4)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.flash_dmla_bwd(q, k, o, o, m, m)

@@ -1,0 +1,128 @@
+"""Parity of the cache-latent backward (dmla_bwd_cache_latent) with fp32 references.
+
+Each case runs this library's forward, then its backward from the saved (o, m, l), and checks
+dq and dk_lat twice:
+  * against the closed-form oracle backward fed with the same o, m, l -- isolates the
+    backward kernels;
+  * against fp32 torch.autograd through the exact forward -- the end-to-end gradient the
+    baseline config 5 names.
+Both at the north-star tolerance (max-abs 2e-2, mean-rel 1e-2).  dk_lat is compared in fp32,
+the op's default output type: its largest entries (a key seen by every later row of all heads
+collects sum_i P_ij dO_i over thousands of rows) reach ~20 at config 5, where a bf16 rounding
+alone is 0.06.  dO ~ N(0, 1) as in config 5.
+"""
+import math
+
+import pytest
+import torch
+
+from conftest import assert_out_close, seeded
+from oracle import dmla_ref as R
+from python import ops
+
+SCALE = 1.0 / math.sqrt(192.0)
+
+
+def _inputs(B, H, Sq, Sk, seed, scale=0.5):
+    q = seeded((B, H, Sq, 576), seed, scale, torch.bfloat16)
+    k = seeded((B, Sk, 576), seed + 1, scale, torch.bfloat16)
+    do = seeded((B, H, Sq, 512), seed + 2, 1.0, torch.bfloat16)
+    return q, k, do
+
+
+def _run(gpu, q, k, do, causal, scale=SCALE, **kw):
+    qg, kg, dog = q.to(gpu), k.to(gpu), do.to(gpu)
+    o, m, l = ops.flash_dmla_fwd(qg, kg, 512, scale, causal)
+    dq, dk = ops.flash_dmla_bwd(qg, kg, o, dog, m, l, 512, scale, causal, **kw)
+    torch.cuda.synchronize()
+    return o, m, l, dq, dk
+
+
+def _check(gpu, q, k, do, causal, scale=SCALE, ref_device="cpu", autograd=True):
+    o, m, l, dq, dk = _run(gpu, q, k, do, causal, scale)
+    assert dq.dtype == torch.bfloat16 and dk.dtype == torch.float32
+    dev = gpu if ref_device == "gpu" else torch.device("cpu")
+    qf, kf, dof = q.to(dev).float(), k.to(dev).float(), do.to(dev).float()
+    dq_ref, dk_ref = R.dmla_bwd_cache_latent(qf, kf, o.to(dev).float(), dof, m.to(dev), l.to(dev), 512, scale,
+                                             causal)
+    assert_out_close(dq, dq_ref, "dq vs oracle backward")
+    assert_out_close(dk, dk_ref, "dk_lat vs oracle backward")
+    if autograd:
+        dq_ag, dk_ag = R.dmla_grads_autograd(qf, kf, dof, 512, scale, causal, torch.float32)
+        assert_out_close(dq, dq_ag, "dq vs fp32 autograd")
+        assert_out_close(dk, dk_ag, "dk_lat vs fp32 autograd")
+    return dq, dk
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize(
+    "B,H,Sq,Sk,causal",
+    [
+        (1, 16, 64, 64, True),      # one key block (a pair with itself), two row tiles
+        (1, 16, 128, 128, True),    # one key-block pair
+        (2, 16, 200, 200, True),    # ragged rows and keys, several pairs
+        (1, 3, 77, 77, True),       # heads not dividing the 32-row tile
+        (1, 1, 130, 130, True),     # one head
+        (2, 16, 96, 96, False),     # non-causal
+        (1, 8, 100, 300, False),    # non-causal, Sq < Sk
+        (1, 8, 40, 100, True),      # Sq < Sk: bottom-right aligned causal
+        (1, 4, 150, 70, True),      # Sq > Sk: the first rows see no key and get no gradient
+        (1, 128, 8, 8, True),       # many heads, few positions
+    ],
+)
+def test_bwd_small_shapes(gpu, B, H, Sq, Sk, causal):
+    q, k, do = _inputs(B, H, Sq, Sk, seed=B * 1000 + H * 10 + Sq)
+    _check(gpu, q, k, do, causal)
+
+
+@pytest.mark.gpu
+def test_bwd_many_segments(gpu):
+    # 16 key blocks, 8 pairs, up to 32 row segments per pair: work items that switch key block
+    # mid-item and dK partials summed across segments.
+    q, k, do = _inputs(1, 16, 1024, 1024, seed=11)
+    _check(gpu, q, k, do, True, ref_device="gpu")
+
+
+@pytest.mark.gpu
+def test_bwd_strided_views_and_fp32_outputs(gpu):
+    qb = seeded((2, 16, 70, 640), 7, 0.5, torch.bfloat16)
+    kb = seeded((2, 70, 704), 8, 0.5, torch.bfloat16)
+    dob = seeded((2, 16, 70, 576), 9, 1.0, torch.bfloat16)
+    q, k, do = qb[..., :576], kb[..., 64:640], dob[..., 32:544]
+    o, m, l, dq, dk = _run(gpu, q, k, do, True, dq_dtype=torch.float32, dk_dtype=torch.bfloat16)
+    assert dq.dtype == torch.float32 and dk.dtype == torch.bfloat16
+    dq_ref, dk_ref = R.dmla_bwd_cache_latent(q.float(), k.float(), o.cpu().float(), do.float(), m.cpu(), l.cpu(),
+                                             512, SCALE, True)
+    assert_out_close(dq, dq_ref, "dq fp32")
+    # bf16 dk_lat: the tolerance plus the rounding of the output type itself (2^-9 relative).
+    diff = (dk.float().cpu() - dk_ref).abs()
+    assert (diff <= 2e-2 + dk_ref.abs() * 2.0 ** -9).all(), f"dk bf16 max diff {diff.max().item():.3e}"
+
+
+@pytest.mark.gpu
+def test_bwd_config5_full_shape(gpu):
+    # B=4, H=16, S=2048, causal, dO ~ N(0, 1); references in fp32 on the GPU.
+    q, k, do = _inputs(4, 16, 2048, 2048, seed=0)
+    _check(gpu, q, k, do, True, ref_device="gpu")
+
+
+@pytest.mark.gpu
+def test_bwd_is_deterministic(gpu):
+    q, k, do = _inputs(2, 16, 300, 300, seed=21)
+    _, _, _, dq1, dk1 = _run(gpu, q, k, do, True)
+    _, _, _, dq2, dk2 = _run(gpu, q, k, do, True)
+    assert torch.equal(dq1, dq2) and torch.equal(dk1, dk2)
+
+
+@pytest.mark.gpu
+def test_autograd_function_matches_fp32_autograd(gpu):
+    q, k, do = _inputs(1, 4, 96, 96, seed=31)
+    qg = q.to(gpu).requires_grad_(True)
+    kg = k.to(gpu).requires_grad_(True)
+    out = ops.flash_dmla(qg, kg, 512, SCALE, True)
+    out.backward(do.to(gpu))
+    assert qg.grad.dtype == torch.bfloat16 and kg.grad.dtype == torch.bfloat16
+    dq_ag, dk_ag = R.dmla_grads_autograd(q.float(), k.float(), do.float(), 512, SCALE, True, torch.float32)
+    assert_out_close(qg.grad, dq_ag, "dq through autograd.Function")
+    diff = (kg.grad.float().cpu() - dk_ag).abs()
+    assert (diff <= 2e-2 + dk_ag.abs() * 2.0 ** -9).all(), f"dk bf16 max diff {diff.max().item():.3e}"
