@@ -41,7 +41,7 @@ constexpr int kOGroups = kDv / 64;                  // 8 chunk groups of a dO ti
 constexpr int kQBytes = kQGroups * kGroupBytes;     // 36 KB
 constexpr int kStageBytes = kQBytes + kOGroups * kGroupBytes;   // 68 KB: Q and dO of one tile
 constexpr int kXOffset = 2 * kStageBytes;           // P^T / dS'^T exchange: [2][4 kb][64 lanes][16 B]
-constexpr int kDkdvLds = kXOffset + 2 * 4 * 1024;   // 144 KB
+constexpr int kDkdvLds = kXOffset + 2 * 4 * 1024 + 4 * 4096;   // 160 KB: stages, exchange, swap
 constexpr int kCb = kDqk / 16;                      // 36 column blocks of dK / dQ
 constexpr int kPartFloats = kKeys * kDqk;           // one dK partial: 64 keys x 576 fp32
 constexpr int kMaxParts = 64;
@@ -64,6 +64,7 @@ struct BwdParams {
   int64_t q_sb, q_sh, q_ss, k_sb, k_ss, o_sb, o_sh, o_ss, do_sb, do_sh, do_ss;
   int64_t dq_sb, dq_sh, dq_ss, dk_sb, dk_ss;
   int B, H, Sq, Sk, causal;
+  FastDiv hdiv;         // row -> position (rows are position * H + head)
   float scale, scale_log2;
   int R;                // H * Sq rows per batch element
   int n_rt;             // 32-row tiles per batch element, even: 2 * ceil(R / 64)
@@ -122,7 +123,7 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(BwdParams p) {
   int pos = 0, h = 0;
   const bool valid = row < p.R;
   if (valid) {
-    pos = row / p.H;
+    pos = fast_div(row, p.hdiv);
     h = row - pos * p.H;
     const bf16* orow = p.o + b * p.o_sb + h * p.o_sh + pos * p.o_ss + 64 * part;
     const bf16* drow = p.dout + b * p.do_sb + h * p.do_sh + pos * p.do_ss + 64 * part;
@@ -183,18 +184,29 @@ __global__ void __launch_bounds__(256) bwd_kt_kernel(BwdParams p) {
 // ---- 3. dK_lat / dV: key-block-stationary sweep over row tiles ----------------------------
 //
 // Workgroup = 4 waves (one per SIMD, up to 512 registers each) on 64 keys.  Per 32-row tile:
-//   S-phase:  wave w computes S and dP for rows 16 (w&1) .. +15 and keys 32 (w>>1) .. +31
-//             (2 x 34 MFMAs), with those keys' K_lat rows held in registers as the B operand
-//             and the rows' Q / dO read from LDS; then P and dS' = scale P (dP - D), masked.
-//             The MFMA C layout (lane: one key, 4 rows) is exactly half of the A operand the
-//             dK update needs (lane: one key, 8 rows), so the two row halves meet in a 4 KB LDS
-//             exchange without any transposition.  dS' also goes to HBM for dQ.
-//   dK-phase: wave w owns column blocks w, w+4, .., w+32 of all 64 keys (36 accumulators):
-//             dK += dS'^T Q (9 blocks) and dK[:, :512] += P^T dO (8 blocks), fp16 operands; Q
-//             and dO columns come from ds_read_b64_tr_b16 so that k runs along the tile's rows.
-// Row tiles stream through two LDS stages (Q + dO = 68 KB each) with direct global->LDS copies;
-// two barriers per tile (tile landed / exchange written).
-__global__ void __launch_bounds__(kBwdThreads, 1) bwd_dkdv_kernel(BwdParams p) {
+//   S-phase:  wave w = (row block rb = w>>1, dim half dh = w&1) computes partial S and dP for
+//             rows 16 rb .. +15 and all 64 keys over its half of the contraction (S: dims
+//             256 dh .. +255 and rope dims 512 + 32 dh .. +31; dP: dims 256 dh .. +255).  The
+//             64 keys' K_lat columns of that half are the B operand, held in the AGPR file (144
+//             registers), so each Q / dO row read from LDS feeds four MFMAs: with one wave per
+//             SIMD the LDS delivers about 1 KB per wave every ~70 cycles, and this halves the
+//             reads per MFMA against two keys blocks per wave.  The pair (rb, 0) / (rb, 1) swaps
+//             the fp32 partials of the key blocks the other one finishes (4 KB each way); wave
+//             (rb, dh) then forms P and dS' = scale P (dP - D), masked, for key blocks 2 dh,
+//             2 dh + 1.  The MFMA C layout (lane: one key, 4 rows) is exactly half of the A
+//             operand the dK update needs (lane: one key, 8 rows), so the two row blocks meet
+//             in a 4 KB exchange without transposition; dS' also goes to HBM for dQ.
+//   dK-phase: wave w owns column blocks w, w+4, .., w+32 of all 64 keys (36 accumulators in
+//             arch VGPRs): dK += dS'^T Q (9 blocks) and dK[:, :512] += P^T dO (8 blocks), fp16
+//             operands; Q and dO columns come from ds_read_b64_tr_b16 so that k runs along
+//             the tile's rows.
+// Row tiles stream through two LDS stages (Q + dO = 68 KB each) with direct global->LDS
+// copies; three barriers per tile (tile landed / partials swapped / exchange written).
+constexpr int kXchOffset = kXOffset + 2 * 4 * 1024;   // partial swap: [wave][4 tiles][64 lanes][16 B]
+static_assert(kXchOffset + 4 * 4096 == kDkdvLds, "LDS layout");
+
+__global__ void __launch_bounds__(kBwdThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
+bwd_dkdv_kernel(BwdParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[kDkdvLds];
   DMLA_LDS char* lds = (DMLA_LDS char*)smem;
   const int wave = uniform(threadIdx.x >> 6);
@@ -211,18 +223,19 @@ __global__ void __launch_bounds__(kBwdThreads, 1) bwd_dkdv_kernel(BwdParams p) {
   const int lo = part_begin(pp.total, p.parts, pj), hi = part_begin(pp.total, p.parts, pj + 1);
 
   const int l16 = lane & 15, g = lane >> 4;
-  const int rb = wave & 1;       // S-phase row block
-  const int kp = wave >> 1;      // S-phase key pair: key blocks 2 kp, 2 kp + 1 of the 64
+  const int rb = wave >> 1;      // S-phase row block
+  const int dh = wave & 1;       // S-phase dim half; this wave finishes key blocks 2 dh, 2 dh + 1
   const int off = p.Sk - p.Sq;
   const float scale = p.scale, scale_log2 = p.scale_log2;
   const unsigned lds_base = lds_addr(lds);
   DMLA_LDS char* xbuf = lds + kXOffset;
+  DMLA_LDS char* xch = lds + kXchOffset;
 
-  // Per-lane LDS offsets (tile-relative).  S-phase A operand (row operand of row block rb):
-  // chunk 4c + g of row 16 rb + l16 = group c/2, in-group chunk 4 (c&1) + g.
+  // Per-lane LDS offsets (tile-relative).  S-phase A operand (row operand) of row block rb and
+  // k-step c (dims 32c ..): chunk 4c + g of row 16 rb + l16 = group c/2, in-group chunk
+  // 4 (c&1) + g.
   const int arow = 16 * rb + l16;
-  const int a_off0 = arow * 128 + 16 * (g ^ swz(arow & 15));
-  const int a_off1 = arow * 128 + 16 * ((4 + g) ^ swz(arow & 15));
+  const int a_off[2] = {arow * 128 + 16 * (g ^ swz(arow & 15)), arow * 128 + 16 * ((4 + g) ^ swz(arow & 15))};
   // dK-phase B operand (column operand) of column block cb = wave + 4u: group u, in-group chunk
   // 2 wave + (q >> 1) of rows 4g + e (+16 for the second half).
   const int e = l16 >> 2, qq = l16 & 3;
@@ -247,18 +260,23 @@ __global__ void __launch_bounds__(kBwdThreads, 1) bwd_dkdv_kernel(BwdParams p) {
     first_segment = false;
     const int key0 = kb * kKeys;
 
-    // K_lat rows of this wave's two key blocks, B operand of S = Q K^T (zero past Sk):
-    // kreg[kk][c] = K[key0 + 32 kp + 16 kk + l16][32 c + 8 g .. +7]
-    bf16x8 kreg[2][18];
+    // K_lat columns of this wave's dim half for all 64 keys, B operand of S = Q K^T (zero past
+    // Sk): kreg[kb][j] = K[key0 + 16 kb + l16][32 step(j) + 8 g .. +7], step(j) = 8 dh + j for
+    // j < 8 (also the V_lat columns of dP) and 16 + dh for j = 8.
+    bf16x8 kreg[4][9];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int key = key0 + 32 * kp + 16 * kk + l16;
+    for (int kbl = 0; kbl < 4; ++kbl) {
+      const int key = key0 + 16 * kbl + l16;
       const bool kvalid = key < p.Sk;
       const bf16* krow = p.k + b * p.k_sb + (int64_t)(kvalid ? key : 0) * p.k_ss + 8 * g;
 #pragma unroll
-      for (int c = 0; c < 18; ++c) {
-        const bf16x8 v = *reinterpret_cast<const bf16x8*>(krow + 32 * c);
-        kreg[kk][c] = kvalid ? v : bf16x8{};
+      for (int j = 0; j < 9; ++j) {
+        const int step = j < 8 ? 8 * dh + j : 16 + dh;
+        const bf16x8 v = *reinterpret_cast<const bf16x8*>(krow + 32 * step);
+        kreg[kbl][j] = kvalid ? v : bf16x8{};
+        // K_lat lives in the AGPR file (MFMA reads A/B operands from AGPRs directly): the arch
+        // VGPRs hold the 144 accumulators and the LDS operands in flight.
+        asm volatile("" : "+a"(kreg[kbl][j]));
       }
     }
 
@@ -268,89 +286,133 @@ __global__ void __launch_bounds__(kBwdThreads, 1) bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
       for (int v = 0; v < 9; ++v) acc[a][v] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Stage row tile rt into LDS stage st (rows past R re-read row R-1: finite, and masked by
-    // their +inf lse2).
-    auto stage = [&](int rt, int st) {
+    // Staging of row tile rt into LDS stage st (rows past R re-read row R-1: finite, and masked
+    // by their +inf lse2): this lane's row sources, then 17 copies (9 Q chunk groups, 8 dO
+    // groups) issued one per S-phase step and one per early dK-phase operand, so the CU's
+    // vector-memory path (about 64 B per clock: ~1000 clocks for the 68 KB tile) works under the
+    // MFMAs instead of stalling the wave in one burst, and the last copy still has the second
+    // half of the dK-phase to land.
+    const char* qsrc = nullptr;
+    const char* osrc = nullptr;
+    unsigned cdst = 0;
+    auto stage_begin = [&](int rt, int st) {
       const int r = min(rt * kRows + crow, p.R - 1);
-      const int pos = r / p.H, h = r - pos * p.H;
-      const char* qsrc = reinterpret_cast<const char*>(p.q + b * p.q_sb + h * p.q_sh + pos * p.q_ss + 8 * cchunk);
-      const char* osrc = reinterpret_cast<const char*>(p.dout + b * p.do_sb + h * p.do_sh + pos * p.do_ss + 8 * cchunk);
-      const unsigned dst = lds_base + st * kStageBytes + wave * 1024;
-#pragma unroll
-      for (int gq = 0; gq < kQGroups; ++gq) dma16_addr(qsrc + 128 * gq, dst + gq * kGroupBytes);
-#pragma unroll
-      for (int go = 0; go < kOGroups; ++go) dma16_addr(osrc + 128 * go, dst + kQBytes + go * kGroupBytes);
+      const int pos = fast_div(r, p.hdiv), h = r - pos * p.H;
+      qsrc = reinterpret_cast<const char*>(p.q + b * p.q_sb + h * p.q_sh + pos * p.q_ss + 8 * cchunk);
+      osrc = reinterpret_cast<const char*>(p.dout + b * p.do_sb + h * p.do_sh + pos * p.do_ss + 8 * cchunk);
+      cdst = lds_base + st * kStageBytes + wave * 1024;
     };
-    // (lse2, D) and key limit of this lane's 4 S-phase rows 32 rt + 16 rb + 4 g + i.
+    auto stage_copy = [&](int i) {   // i < 9: Q chunk group i; else dO chunk group i - 9
+      if (i < kQGroups) dma16_addr(qsrc + 128 * i, cdst + i * kGroupBytes);
+      else dma16_addr(osrc + 128 * (i - kQGroups), cdst + kQBytes + (i - kQGroups) * kGroupBytes);
+    };
+    // (lse2, D) and key limit of this lane's 4 rows 32 rt + 16 rb + 4 g + i.
     float lse2[4], dval[4];
     int lim[4];
-    auto row_stats = [&](int rt, float (&ls)[4], float (&dv)[4], int (&lm)[4]) {
+    auto row_stats = [&](int rt) {
       const int r0 = rt * kRows + 16 * rb + 4 * g;
       const float4* src = reinterpret_cast<const float4*>(p.lsed + (int64_t)b * p.n_rt * kRows + r0);
       const float4 a0 = src[0], a1 = src[1];
-      ls[0] = a0.x; dv[0] = a0.y; ls[1] = a0.z; dv[1] = a0.w;
-      ls[2] = a1.x; dv[2] = a1.y; ls[3] = a1.z; dv[3] = a1.w;
+      lse2[0] = a0.x; dval[0] = a0.y; lse2[1] = a0.z; dval[1] = a0.w;
+      lse2[2] = a1.x; dval[2] = a1.y; lse2[3] = a1.z; dval[3] = a1.w;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = r0 + i;
-        const int pos = r / p.H;
-        lm[i] = r >= p.R ? -1 : (p.causal ? min(pos + off, p.Sk - 1) : p.Sk - 1);
+        const int pos = fast_div(r, p.hdiv);
+        lim[i] = r >= p.R ? -1 : (p.causal ? min(pos + off, p.Sk - 1) : p.Sk - 1);
       }
     };
 
-    stage(rt_first, 0);
-    row_stats(rt_first, lse2, dval, lim);
+    stage_begin(rt_first, 0);
+#pragma unroll
+    for (int i = 0; i < kQGroups + kOGroups; ++i) stage_copy(i);
+    row_stats(rt_first);
     for (int s = 0; s < count; ++s) {
       const int rt = rt_first + dir * s;
       const int st = s & 1;
       wait_vmem();
-      __syncthreads();   // tile s landed everywhere; the other stage and the exchange are free
-      float lse2n[4], dvaln[4];
-      int limn[4];
-      if (s + 1 < count) {
-        stage(rt + dir, st ^ 1);
-        row_stats(rt + dir, lse2n, dvaln, limn);
-      }
+      __syncthreads();   // tile s landed everywhere; the other stage and the exchanges are free
+      const bool more = s + 1 < count;
+      // The copies run unconditionally (branch-free loop body): past the segment's last tile they
+      // re-read this tile into the idle stage, and the segment end waits for them.
+      stage_begin(more ? rt + dir : rt, st ^ 1);
       const DMLA_LDS char* qt = lds + st * kStageBytes;
       const DMLA_LDS char* ot = qt + kQBytes;
 
-      // ---- S-phase ----
-      f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-      f32x4 pacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+      // ---- S-phase: partial S (9 reads, 36 MFMAs) and dP (8 reads, 32 MFMAs) ----
+      // Step j < 8 reads Q and dO of row block rb at dims 32 (8 dh + j) and feeds 8 MFMAs into
+      // 8 different accumulators (S and dP x 4 key blocks); step 8 is Q's rope slice.  Reads
+      // run two steps ahead of their MFMAs.
+      f32x4 sacc[4], pacc[4];
 #pragma unroll
-      for (int c = 0; c < 18; ++c) {
-        const bf16x8 a = lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(
-            qt + (c >> 1) * kGroupBytes + ((c & 1) ? a_off1 : a_off0)));
-        sacc[0] = mfma_bf16(a, kreg[0][c], sacc[0]);
-        sacc[1] = mfma_bf16(a, kreg[1][c], sacc[1]);
+      for (int kbl = 0; kbl < 4; ++kbl) sacc[kbl] = pacc[kbl] = f32x4{0.f, 0.f, 0.f, 0.f};
+      auto s_read = [&](const DMLA_LDS char* base, int j) -> bf16x8 {
+        const int step = j < 8 ? 8 * dh + j : 16 + dh;
+        return lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(base + (step >> 1) * kGroupBytes + a_off[step & 1]));
+      };
+      bf16x8 qa[3], oa[3];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        qa[j] = s_read(qt, j);
+        oa[j] = s_read(ot, j);
       }
 #pragma unroll
-      for (int c = 0; c < 16; ++c) {
-        const bf16x8 a = lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(
-            ot + (c >> 1) * kGroupBytes + ((c & 1) ? a_off1 : a_off0)));
-        pacc[0] = mfma_bf16(a, kreg[0][c], pacc[0]);
-        pacc[1] = mfma_bf16(a, kreg[1][c], pacc[1]);
+      for (int j = 0; j < 9; ++j) {
+        if (j + 2 < 9) {
+          qa[(j + 2) % 3] = s_read(qt, j + 2);
+          if (j + 2 < 8) oa[(j + 2) % 3] = s_read(ot, j + 2);
+        }
+#pragma unroll
+        for (int kbl = 0; kbl < 4; ++kbl) {
+          sacc[kbl] = mfma_bf16(qa[j % 3], kreg[kbl][j], sacc[kbl]);
+          if (j < 8) pacc[kbl] = mfma_bf16(oa[j % 3], kreg[kbl][j], pacc[kbl]);
+        }
+        stage_copy(j);   // the next tile's Q chunk group j into the other stage
       }
-      // P and dS' for keys key0 + 32 kp + 16 kk + l16, rows 16 rb + 4 g + i of the tile.
+      // Swap: send the partials of the key blocks the partner finishes (2 (1 - dh), +1),
+      // [wave][tile][lane] x 16 B; selects rather than indexing by the wave-dependent dh, which
+      // the compiler would turn into register-indexed moves.
+      f32x4 s_own[2], p_own[2];
+      {
+        DMLA_LDS f32x4* dst = reinterpret_cast<DMLA_LDS f32x4*>(xch + wave * 4096) + lane;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          s_own[kk] = dh ? sacc[2 + kk] : sacc[kk];
+          p_own[kk] = dh ? pacc[2 + kk] : pacc[kk];
+          dst[64 * kk] = dh ? sacc[kk] : sacc[2 + kk];
+          dst[128 + 64 * kk] = dh ? pacc[kk] : pacc[2 + kk];
+        }
+      }
+      __syncthreads();   // partials swapped
+      {
+        const DMLA_LDS f32x4* src = reinterpret_cast<const DMLA_LDS f32x4*>(xch + (wave ^ 1) * 4096) + lane;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          s_own[kk] += src[64 * kk];
+          p_own[kk] += src[128 + 64 * kk];
+        }
+      }
+      // P and dS' for keys key0 + 32 dh + 16 kk + l16, rows 16 rb + 4 g + i of the tile.
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const int key = key0 + 32 * kp + 16 * kk + l16;
+        const int key = key0 + 32 * dh + 16 * kk + l16;
         float pv[4], dsv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float pr = key <= lim[i] ? fast_exp2(sacc[kk][i] * scale_log2 - lse2[i]) : 0.f;
+          const float pr = key <= lim[i] ? fast_exp2(s_own[kk][i] * scale_log2 - lse2[i]) : 0.f;
           pv[i] = pr;
-          dsv[i] = scale * pr * (pacc[kk][i] - dval[i]);
+          dsv[i] = scale * pr * (p_own[kk][i] - dval[i]);
         }
         const f16x4 pb = to_f16x4(pv[0], pv[1], pv[2], pv[3]);
         const f16x4 db = to_f16x4(dsv[0], dsv[1], dsv[2], dsv[3]);
-        const int kbl = 2 * kp + kk;
+        const int kbl = 2 * dh + kk;
         *reinterpret_cast<DMLA_LDS f16x4*>(xbuf + kbl * 1024 + lane * 16 + 8 * rb) = pb;
         *reinterpret_cast<DMLA_LDS f16x4*>(xbuf + 4096 + kbl * 1024 + lane * 16 + 8 * rb) = db;
         _Float16* dsblk = p.ds + ((((int64_t)b * 2 * p.n_rt + 2 * rt + rb) * (4 * p.n_kb)) + 4 * kb + kbl) * 256;
         *reinterpret_cast<f16x4*>(dsblk + 4 * lane) = db;
       }
       __syncthreads();   // exchange written
+      if (more) row_stats(rt + dir);
 
       // ---- dK-phase ----
       f16x8 pT[4], dsT[4];
@@ -358,32 +420,45 @@ __global__ void __launch_bounds__(kBwdThreads, 1) bwd_dkdv_kernel(BwdParams p) {
       for (int kbl = 0; kbl < 4; ++kbl) {
         pT[kbl] = *reinterpret_cast<const DMLA_LDS f16x8*>(xbuf + kbl * 1024 + lane * 16);
         dsT[kbl] = *reinterpret_cast<const DMLA_LDS f16x8*>(xbuf + 4096 + kbl * 1024 + lane * 16);
+        asm volatile("" : "+a"(pT[kbl]));   // A operands of the whole phase: AGPR file
+        asm volatile("" : "+a"(dsT[kbl]));
       }
+      // Column operands of column block wave + 4v (v < 9: Q; v >= 9: dO block v - 9), as two
+      // transposed half reads each; read in batches of 3 operands ahead of their MFMAs.
+      auto k_read = [&](int v, bf16x4& lo, bf16x4& hi) {
+        const DMLA_LDS char* c = v < 9 ? qt + v * kGroupBytes + b_off : ot + (v - 9) * kGroupBytes + b_off;
+        lo = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(c));
+        hi = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(c + 16 * 128));
+      };
+      bf16x4 kl[2][3], kh[2][3];
 #pragma unroll
-      for (int v = 0; v < 9; ++v) {
-        const DMLA_LDS char* qc = qt + v * kGroupBytes + b_off;
-        const f16x8 qb = bf16_to_f16(lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(qc)),
-                                     lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(qc + 16 * 128)));
+      for (int j = 0; j < 3; ++j) k_read(j, kl[0][j], kh[0][j]);
 #pragma unroll
-        for (int kbl = 0; kbl < 4; ++kbl) acc[kbl][v] = mfma_f16(dsT[kbl], qb, acc[kbl][v]);
-        if (v < 8) {
-          const DMLA_LDS char* oc = ot + v * kGroupBytes + b_off;
-          const f16x8 ob = bf16_to_f16(lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(oc)),
-                                       lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(oc + 16 * 128)));
+      for (int bt = 0; bt < 6; ++bt) {   // operands 0..16 in batches of 3 (the last holds 2)
+        if (bt + 1 < 6) {
 #pragma unroll
-          for (int kbl = 0; kbl < 4; ++kbl) acc[kbl][v] = mfma_f16(pT[kbl], ob, acc[kbl][v]);
+          for (int j = 0; j < 3; ++j)
+            if (3 * (bt + 1) + j < 17) k_read(3 * (bt + 1) + j, kl[(bt + 1) & 1][j], kh[(bt + 1) & 1][j]);
         }
-      }
-      if (s + 1 < count) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          lse2[i] = lse2n[i];
-          dval[i] = dvaln[i];
-          lim[i] = limn[i];
+        for (int j = 0; j < 3; ++j) {
+          const int v = 3 * bt + j;
+          if (v < 17) {
+            if (v < kOGroups) stage_copy(kQGroups + v);   // the next tile's dO chunk group v
+            const f16x8 bop = bf16_to_f16(kl[bt & 1][j], kh[bt & 1][j]);
+            if (v < 9) {
+#pragma unroll
+              for (int kbl = 0; kbl < 4; ++kbl) acc[kbl][v] = mfma_f16(dsT[kbl], bop, acc[kbl][v]);
+            } else {
+#pragma unroll
+              for (int kbl = 0; kbl < 4; ++kbl) acc[kbl][v - 9] = mfma_f16(pT[kbl], bop, acc[kbl][v - 9]);
+            }
+          }
         }
       }
     }
 
+    wait_vmem();   // no copy may still land in a stage once the segment is over
     // Partial of this segment: acc[kbl][v] holds dK[16 kbl + 4 g + i][16 (wave + 4 v) + l16].
     float* dst = p.part + ((int64_t)u * 2 + ph) * kPartFloats;
 #pragma unroll
@@ -472,7 +547,7 @@ __global__ void __launch_bounds__(kBwdThreads, 1) bwd_dq_kernel(BwdParams p) {
     for (int i = 0; i < 4; ++i) {
       const int r = row0 + 16 * rq + 4 * g + i;
       if (r >= p.R) continue;
-      const int pos = r / p.H, h = r - pos * p.H;
+      const int pos = fast_div(r, p.hdiv), h = r - pos * p.H;
       const int64_t base = b * p.dq_sb + h * p.dq_sh + pos * p.dq_ss + l16;
 #pragma unroll
       for (int v = 0; v < 9; ++v) {
@@ -615,6 +690,7 @@ extern "C" int dmla_bwd_cache_latent(const void* q, const void* k_lat, const voi
   p.dk_sb = dk_sb; p.dk_ss = dk_ss;
   p.B = (int)B; p.H = (int)H; p.Sq = (int)Sq; p.Sk = (int)Sk;
   p.causal = causal ? 1 : 0;
+  p.hdiv = make_fastdiv((unsigned)H);
   p.scale = softmax_scale;
   p.scale_log2 = softmax_scale * kLog2e;
   p.R = pl.R; p.n_rt = pl.n_rt; p.n_kb = pl.n_kb; p.n_pairs = pl.n_pairs; p.parts = pl.parts;

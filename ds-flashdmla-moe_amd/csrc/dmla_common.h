@@ -137,6 +137,28 @@ __device__ __forceinline__ int col_operand_off(int lane, int cb, int half) {
   return tile_chunk_off(row, 2 * cb + (q >> 1)) + 8 * (q & 1);
 }
 
+// Division of 0 <= n < 2^31 by a runtime divisor d >= 1 with one multiply-high.  With
+// s = ceil(log2 d) and m = floor(2^(31+s) / d) + 1 (< 2^32), n / d = umulhi(n, m) >> (s - 1):
+// m d = 2^(31+s) + e with 0 < e <= d, so the quotient's error term n e / (d 2^(31+s)) stays
+// below 2^-s <= 1/d, less than the distance from n/d to the next integer.  d = 1 (m = 0) is the
+// identity.
+struct FastDiv {
+  unsigned m;
+  int shift;   // s - 1
+};
+inline FastDiv make_fastdiv(unsigned d) {
+  FastDiv f = {0u, 0};
+  if (d <= 1) return f;
+  int s = 0;
+  while ((1ull << s) < d) ++s;
+  f.m = (unsigned)((1ull << (31 + s)) / d + 1);
+  f.shift = s - 1;
+  return f;
+}
+__device__ __forceinline__ int fast_div(int n, FastDiv f) {
+  return f.m ? (int)(__umulhi((unsigned)n, f.m) >> f.shift) : n;
+}
+
 // Reductions over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48: the lanes that
 // share one MFMA column) with the gfx950 row-swap instructions.  Called with the same value in
 // both operands, permlane16_swap / permlane32_swap return, in some order, a lane's value and
