@@ -113,7 +113,9 @@ __device__ __forceinline__ f16x4 to_f16x4(float a, float b, float c, float d) {
 }
 
 // ---- 1. row statistics -------------------------------------------------------------------
-// One workgroup per 32-row tile; 8 lanes per row, each summing 64 products of dO * O.
+// One workgroup per 32-row tile; 8 lanes per row.  Load c of lane p covers elements
+// 8 (8c + p) .. +7, so the 8 lanes of a row read 128 contiguous bytes per instruction, and
+// each lane keeps 16 loads in flight.
 __global__ void __launch_bounds__(256) bwd_prep_kernel(BwdParams p) {
   const int b = blockIdx.y;
   const int t = threadIdx.x;
@@ -125,15 +127,18 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(BwdParams p) {
   if (valid) {
     pos = fast_div(row, p.hdiv);
     h = row - pos * p.H;
-    const bf16* orow = p.o + b * p.o_sb + h * p.o_sh + pos * p.o_ss + 64 * part;
-    const bf16* drow = p.dout + b * p.do_sb + h * p.do_sh + pos * p.do_ss + 64 * part;
+    const bf16* orow = p.o + b * p.o_sb + h * p.o_sh + pos * p.o_ss + 8 * part;
+    const bf16* drow = p.dout + b * p.do_sb + h * p.do_sh + pos * p.do_ss + 8 * part;
+    bf16x8 ov[8], dv[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      const bf16x8 ov = *reinterpret_cast<const bf16x8*>(orow + 8 * c);
-      const bf16x8 dv = *reinterpret_cast<const bf16x8*>(drow + 8 * c);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dsum += (float)ov[e] * (float)dv[e];
+      ov[c] = *reinterpret_cast<const bf16x8*>(orow + 64 * c);
+      dv[c] = *reinterpret_cast<const bf16x8*>(drow + 64 * c);
     }
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dsum += (float)ov[c][e] * (float)dv[c][e];
   }
   dsum += __shfl_xor(dsum, 1, 8);
   dsum += __shfl_xor(dsum, 2, 8);
