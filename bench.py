@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Flash-DMLA benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--secondary decode,bwd] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--secondary decode,bwd,onthefly] [--no-cpu-baseline]
 
 Primary line (BASELINE.json metric, config 2): cache-latent DMLA prefill forward, bf16, causal,
 B=4, H=16, S=2048, Q [B,H,S,576], shared K_lat [B,S,576], V_lat = K_lat[..., :512], scale
@@ -14,8 +14,9 @@ counting B*H*S(S+1)*(576+512) flops (unmasked causal pairs only).
 `cpu_baseline` times the fp32 PyTorch eager oracle (oracle/dmla_ref.py) on the host cores
 (at most 16 threads) over the same workload, repeated for about --cpu-seconds seconds.
 `secondary` carries the paged decode (config 3) in KV GB/s with its own HBM roofline, timed
-the same way with rotating KV pools larger than the 256 MB MALL, and the cache-latent backward
-(config 5) in TFLOP/s, counting B*H*S(S+1)*(3*576+2*512) flops.
+the same way with rotating KV pools larger than the 256 MB MALL, the cache-latent backward
+(config 5) in TFLOP/s, counting B*H*S(S+1)*(3*576+2*512) flops, and the on-the-fly forward
+(config 4) in TFLOP/s, counting B*H*S(S+1)*128 + 4*B*S*H*128*64 flops (projection once).
 """
 import argparse
 import json
@@ -217,6 +218,59 @@ def cpu_decode(q, pool, table, lens, bytes_total, budget_s):
             "seconds": t}
 
 
+def bench_onthefly(steps, warmup, cpu_baseline):
+    """Config 4: on-the-fly forward, projections inside the kernel."""
+    import torch
+
+    from python import ops
+
+    B, H, S = 2, 32, 4096
+    dev = torch.device("cuda:0")
+    q = _seeded((B, H, S, 64), 10, 1.0, torch.bfloat16).to(dev)
+    k = _seeded((B, S, H, 128), 11, 1.0, torch.bfloat16).to(dev)
+    v = _seeded((B, S, H, 128), 12, 1.0, torch.bfloat16).to(dev)
+    bound = math.sqrt(6.0 / (128 + 64))
+    g = torch.Generator().manual_seed(13)
+    wk = ((torch.rand(H, 128, 64, generator=g) * 2 - 1) * bound).to(torch.bfloat16).to(dev)
+    wv = ((torch.rand(H, 128, 64, generator=g) * 2 - 1) * bound).to(torch.bfloat16).to(dev)
+    # Attention B*H*S(S+1)*128 plus the projections counted once, 2 * (2*B*S*H*128*64).
+    flops = B * H * S * (S + 1) * 128 + 2 * (2 * B * S * H * 128 * 64)
+
+    def step(i=0):
+        ops.flash_dmla_fwd_onthefly(q, k, v, wk, wv, 0.125, True)
+
+    wall_ms, kern_ms = _time_launches(step, steps, warmup)
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    res = {
+        "metric": "DMLA on-the-fly prefill TFLOP/s (config 4)",
+        "value": flops / (wall_ms * 1e-3) / 1e12,
+        "unit": "TFLOP/s",
+        "ms_per_step": wall_ms,
+        "config": {"workload": "on-the-fly prefill fwd (BASELINE config 4)", "batch": B, "heads": H, "seq_len": S,
+                   "d_in": 128, "d_lat": 64, "causal": True, "softmax_scale": 0.125},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": _load_traffic("onthefly"),
+                     "kernel": "otf_fwd_kernel", "kernel_ms": kern_ms, "algorithmic_flops_per_launch": flops},
+    }
+    if cpu_baseline:
+        res["cpu_baseline"] = cpu_onthefly(q.cpu(), k.cpu(), v.cpu(), wk.cpu(), wv.cpu(), flops, cpu_baseline)
+    return res
+
+
+def cpu_onthefly(q, k, v, wk, wv, flops, budget_s):
+    """fp32 eager oracle (projection + exact attention) on batch element 0, repeated ~budget_s."""
+    import torch
+
+    from oracle import dmla_ref as R
+
+    torch.set_num_threads(_cpu_threads())
+    qf, kf, vf, wkf, wvf = q[:1].float(), k[:1].float(), v[:1].float(), wk.float(), wv.float()
+    n, t = _time_repeated(lambda: R.dmla_fwd_onthefly(qf, kf, vf, wkf, wvf, 0.125, True), budget_s)
+    return {"value": n * flops / q.shape[0] / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"config 4 batch element 0 through the fp32 eager oracle, {n} passes in {t:.1f} s",
+            "seconds": t}
+
+
 def bench_bwd(steps, warmup, cpu_baseline):
     """Config 5: cache-latent backward (all its kernels) from one forward's saved o, m, l."""
     import torch
@@ -287,7 +341,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=30)
-    ap.add_argument("--secondary", default="decode,bwd", help="comma list of extra workloads: decode, bwd")
+    ap.add_argument("--secondary", default="decode,bwd,onthefly",
+                    help="comma list of extra workloads: decode, bwd, onthefly")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget per workload")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -314,6 +369,8 @@ def main():
             secondary["decode"] = bench_decode(args.steps, args.warmup, cpu)
         elif name == "bwd":
             secondary["bwd"] = bench_bwd(args.steps, args.warmup, cpu)
+        elif name == "onthefly":
+            secondary["onthefly"] = bench_onthefly(args.steps, args.warmup, cpu)
         else:
             raise SystemExit(f"unknown secondary workload {name}")
     line = {

@@ -8,5 +8,6 @@ from .ops import (  # noqa: F401
     flash_dmla_bwd,
     flash_dmla_decode_paged,
     flash_dmla_fwd,
+    flash_dmla_fwd_onthefly,
 )
 from ._lib import DmlaError, DmlaInvalidArgument, DmlaUnsupported  # noqa: F401

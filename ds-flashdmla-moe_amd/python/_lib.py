@@ -52,6 +52,13 @@ SIGNATURES = {
         + [_i64] * 8  # q_sb q_sh q_ss k_sb k_ss o_sb o_sh o_ss
         + [_f32, _int, _ptr],  # scale, causal, stream
     ),
+    "dmla_fwd_onthefly": (
+        _int,
+        [_ptr] * 8  # q, k, v, wk, wv, o, m, l
+        + [_i64] * 6  # B, H, Sq, Sk, d_in, d_lat
+        + [_i64] * 14  # q(3) k(3) v(3) w(2) o(3) strides
+        + [_f32, _int, _ptr],  # scale, causal, stream
+    ),
     "dmla_decode_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "dmla_decode_paged": (
         _int,

@@ -89,6 +89,50 @@ def flash_dmla_fwd(
     return o, m, l
 
 
+def flash_dmla_fwd_onthefly(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    wk: torch.Tensor,
+    wv: torch.Tensor,
+    softmax_scale: Optional[float] = None,
+    causal: bool = True,
+    return_stats: bool = False,
+):
+    """On-the-fly DMLA forward: K_lat = K WK and V_lat = V WV per head inside the kernel.
+
+    q [B, H, Sq, 64]; k, v [B, Sk, H, 128]; wk, wv [H, 128, 64] (all bf16).  Returns o
+    [B, H, Sq, 64] bf16, or (o, m, l) with return_stats.  softmax_scale defaults to 1/sqrt(64).
+    """
+    _check_bf16("q", q, 4)
+    for name, t in (("k", k), ("v", v)):
+        _check_bf16(name, t, 4)
+    for name, t in (("wk", wk), ("wv", wv)):
+        _check_bf16(name, t, 3)
+    B, H, Sq, Dl = q.shape
+    Sk, Din = k.shape[1], k.shape[3]
+    _require(tuple(k.shape) == (B, Sk, H, Din) and tuple(v.shape) == (B, Sk, H, Din),
+             "k and v must both be [B, Sk, H, d_in] with q's B and H")
+    _require(tuple(wk.shape) == (H, Din, Dl) and tuple(wv.shape) == (H, Din, Dl),
+             "wk and wv must be [H, d_in, d_lat]")
+    _require(wk.stride() == wv.stride(), "wk and wv must share strides")
+    o = torch.empty((B, H, Sq, Dl), dtype=torch.bfloat16, device=q.device)
+    m = l = None
+    if return_stats:
+        m = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device)
+        l = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device)
+    _lib.call(
+        "dmla_fwd_onthefly",
+        _ptr(q), _ptr(k), _ptr(v), _ptr(wk), _ptr(wv), _ptr(o), _ptr(m), _ptr(l),
+        B, H, Sq, Sk, Din, Dl,
+        q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
+        v.stride(0), v.stride(1), v.stride(2), wk.stride(0), wk.stride(1),
+        o.stride(0), o.stride(1), o.stride(2),
+        _scale(softmax_scale, Dl), 1 if causal else 0, _stream(q),
+    )
+    return (o, m, l) if return_stats else o
+
+
 def flash_dmla_decode_paged(
     q: torch.Tensor,
     kv_pool: torch.Tensor,

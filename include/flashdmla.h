@@ -68,6 +68,30 @@ int dmla_fwd_cache_latent(const void* q, const void* k_lat, void* o, float* m, f
                           float softmax_scale, int causal, dmla_stream_t stream);
 
 /*
+ * On-the-fly DMLA forward (prefill): per-head latent projections inside the kernel.
+ * Replaces: fa2_forward (csrc/attention/fa2_fwd.cu:139-156) in the on-the-fly mode of
+ * README.md:14 -- the role of the absent csrc/attention/fa2_dmla_fwd.cu (README.md:45).
+ *
+ *   q      [B, H, Sq, d_lat]   bf16  strides (q_sb, q_sh, q_ss)
+ *   k, v   [B, Sk, H, d_in]    bf16  strides (k_sb, k_ss, k_sh), (v_sb, v_ss, v_sh)
+ *   wk, wv [H, d_in, d_lat]    bf16  strides (w_sh, w_si, 1), shared by both
+ *   o      [B, H, Sq, d_lat]   bf16  strides (o_sb, o_sh, o_ss)
+ *   m, l   [B, H, Sq]          fp32  contiguous; may both be NULL
+ *
+ *   K_lat[b,h] = k[b,:,h,:] wk[h] and V_lat[b,h] = v[b,:,h,:] wv[h] (rounded to bf16 inside
+ *   the kernel), then o = softmax(softmax_scale q K_lat^T (+ causal mask)) V_lat with the
+ *   statistics of dmla_fwd_cache_latent (natural-log units; m = -inf, l = 0, o = 0 for a row
+ *   without an unmasked key).  causal != 0 masks key j > i + (Sk - Sq).
+ * Supported: d_in = 128, d_lat = 64.
+ */
+int dmla_fwd_onthefly(const void* q, const void* k, const void* v, const void* wk, const void* wv,
+                      void* o, float* m, float* l, int64_t B, int64_t H, int64_t Sq, int64_t Sk,
+                      int64_t d_in, int64_t d_lat, int64_t q_sb, int64_t q_sh, int64_t q_ss,
+                      int64_t k_sb, int64_t k_ss, int64_t k_sh, int64_t v_sb, int64_t v_ss,
+                      int64_t v_sh, int64_t w_sh, int64_t w_si, int64_t o_sb, int64_t o_sh,
+                      int64_t o_ss, float softmax_scale, int causal, dmla_stream_t stream);
+
+/*
  * Paged-KV DMLA decode (one query token per sequence).
  * No reference counterpart exists (the reference has no paged decode); it is the decode form
  * of fa2_forward (fa2_fwd.cu:139-156) over the latent cache.
