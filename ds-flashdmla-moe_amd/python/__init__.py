@@ -4,6 +4,7 @@ from .ops import (  # noqa: F401
     D_V,
     PAGE_SIZE,
     FlashDMLACacheLatent,
+    FlashDMLAOnTheFly,
     flash_dmla,
     flash_dmla_bwd,
     flash_dmla_decode_paged,

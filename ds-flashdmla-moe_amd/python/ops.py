@@ -275,6 +275,22 @@ def flash_dmla_bwd(
     return dq, dk
 
 
+class FlashDMLAOnTheFly(torch.autograd.Function):
+    """o = FlashDMLAOnTheFly.apply(q, k, v, wk, wv, softmax_scale, causal).
+
+    Forward only: the gradients of the on-the-fly mode (dq, dk, dv, dwk, dwv) are not built
+    into this library, and backward raises instead of returning something approximate.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, wk, wv, softmax_scale=None, causal=True):
+        return flash_dmla_fwd_onthefly(q, k, v, wk, wv, softmax_scale, causal)
+
+    @staticmethod
+    def backward(ctx, do):
+        raise NotImplementedError("FlashDMLAOnTheFly: the on-the-fly backward is not built into this library")
+
+
 def flash_dmla(q, k_lat, d_v=D_V, softmax_scale=None, causal=True):
     """Differentiable cache-latent DMLA attention (functional form of FlashDMLACacheLatent)."""
     return FlashDMLACacheLatent.apply(q, k_lat, d_v, softmax_scale, causal)

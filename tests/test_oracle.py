@@ -188,7 +188,7 @@ def _mutant_bwd(q, k, o, do, m, l, d_v, scale, mistake):
     v = k[0, :, :d_v]
     delta = (do[0] * o[0]).sum(-1)
     dp = do[0] @ v.t()
-    ds = p * (dp - delta.unsqueeze(-1))
+    ds = p * dp if mistake == "no_delta" else p * (dp - delta.unsqueeze(-1))
     dq_scale = 1.0 if mistake == "dq_no_scale" else scale
     dq = dq_scale * ds @ k[0]
     dk = scale * (ds.transpose(-1, -2) @ q[0]).sum(0)
@@ -197,7 +197,7 @@ def _mutant_bwd(q, k, o, do, m, l, d_v, scale, mistake):
     return dq.unsqueeze(0), dk.unsqueeze(0)
 
 
-@pytest.mark.parametrize("mistake", ["dq_no_scale", "no_v_fold"])
+@pytest.mark.parametrize("mistake", ["dq_no_scale", "no_v_fold", "no_delta"])
 def test_planted_backward_mistakes_are_caught(mistake):
     g = _golden()
     q, k, do = (torch.from_numpy(g[n]).double() for n in ("q", "k_lat", "do"))
@@ -207,7 +207,7 @@ def test_planted_backward_mistakes_are_caught(mistake):
     assert bad, f"golden gradients failed to catch the planted mistake {mistake}"
 
 
-@pytest.mark.parametrize("mistake", ["v_wrong_slice", "k_transposed_dims", "unscaled_m"])
+@pytest.mark.parametrize("mistake", ["v_wrong_slice", "k_transposed_dims", "unscaled_m", "mask_off_by_one"])
 def test_planted_forward_mistakes_are_caught(mistake):
     g = _golden()
     q, k = torch.from_numpy(g["q"]).double(), torch.from_numpy(g["k_lat"]).double()
@@ -215,6 +215,14 @@ def test_planted_forward_mistakes_are_caught(mistake):
         o, m, l = R.attention_exact(q[0], k, k[..., -32:], 1 / 8, True)
     elif mistake == "k_transposed_dims":
         o, m, l = R.attention_exact(q[0], k.flip(-1), k[..., :32], 1 / 8, True)
+    elif mistake == "mask_off_by_one":   # each row also sees the next key
+        s = (q[0] @ k.transpose(-1, -2)) / 8
+        n = s.shape[-1]
+        mask = torch.arange(n).view(1, n) > torch.arange(n).view(n, 1) + 1
+        s = s.masked_fill(mask, float("-inf"))
+        m = s.amax(-1)
+        p = torch.exp(s - m.unsqueeze(-1))
+        o = (p / p.sum(-1, keepdim=True)) @ k[0, :, :32]
     else:
         o, m, l = R.attention_exact(q[0], k, k[..., :32], 1 / 8, True)
         m = m * 8.0
