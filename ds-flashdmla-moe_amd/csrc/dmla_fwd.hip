@@ -586,7 +586,9 @@ int decode_pages_per_split(int64_t B, int64_t H, int64_t max_pages) {
   const int64_t cus = device_cu_count();
   const int64_t hg = (H + kRowsPerWG - 1) / kRowsPerWG;
   const int64_t total = B * hg * max_pages;
-  int64_t pps = (total + 2 * cus - 1) / (2 * cus);
+  // About one split per CU at full length: measured on cfg 3, smaller splits lose more to the
+  // per-split prologue (Q, first-tile max) and the fp32 partials than they gain in balance.
+  int64_t pps = (total + cus - 1) / cus;
   if (pps < 2) pps = 2;
   if (pps > max_pages) pps = max_pages;
   if (pps > kMaxSplitPages) pps = kMaxSplitPages;
