@@ -192,7 +192,7 @@ def bench_decode(steps, warmup, cpu_baseline):
                    "ctx_sum": int(lens.sum()), "ctx_min": int(lens.min()), "ctx_max": int(lens.max())},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": _load_traffic("decode"),
-                     "kernel": "mqa_fwd_kernel<true> + decode_combine_kernel", "kernel_ms": kern_ms,
+                     "kernel": "mqa_fwd_kernel<true> + lse_combine_kernel", "kernel_ms": kern_ms,
                      "algorithmic_bytes_per_launch": bytes_total},
     }
     if cpu_baseline:

@@ -551,37 +551,7 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
   else mqa_fwd_body<kDecode, 1, false>(p, params, wk, lds, wave, lane);
 }
 
-// Merges the normalised split partials of one (sequence, head): o = sum_s w_s o_s / sum_s w_s
-// with w_s = exp(lse_s - max lse).  One 128-thread block per (b, h), 4 columns per thread.
-__global__ __launch_bounds__(128) void decode_combine_kernel(MqaParams p) {
-  const int b = blockIdx.x / p.H, h = blockIdx.x % p.H;
-  const int ctx = min(max(p.seqlens[b], 0), p.max_pages * kPage);
-  const int npages = (ctx + kPage - 1) / kPage;
-  const int nsplit = max(1, (npages + p.pages_per_split - 1) / p.pages_per_split);
-  if (nsplit == 1) return;
-  const int64_t base = (int64_t)b * p.max_splits * p.H + h;
-  float mx = kNegInf;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, p.part_lse[base + (int64_t)s * p.H]);
-  const float mref = mx == kNegInf ? 0.f : mx;
-  float wsum = 0.f;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const int col = threadIdx.x * 4;
-  for (int s = 0; s < nsplit; ++s) {
-    const int64_t slot = base + (int64_t)s * p.H;
-    const float w = __expf(p.part_lse[slot] - mref);
-    wsum += w;
-    acc += w * *reinterpret_cast<const f32x4*>(p.part_o + slot * kDv + col);
-  }
-  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  acc *= inv;
-  bf16x4 w4;
-  w4[0] = (bf16)acc[0]; w4[1] = (bf16)acc[1]; w4[2] = (bf16)acc[2]; w4[3] = (bf16)acc[3];
-  *reinterpret_cast<bf16x4*>(p.o + b * p.o_sb + h * p.o_sh + col) = w4;
-  if (threadIdx.x == 0 && p.lse != nullptr) p.lse[b * p.H + h] = wsum > 0.f ? mref + __logf(wsum) : mx;
-}
-
-// Pages per split for a decode batch: enough splits to give every CU about two workgroups'
-// worth of pages when all sequences are at full length.
+// Pages per split for a decode batch (at least 2, at most the table width).
 int decode_pages_per_split(int64_t B, int64_t H, int64_t max_pages) {
   const int64_t cus = device_cu_count();
   const int64_t hg = (H + kRowsPerWG - 1) / kRowsPerWG;
@@ -723,6 +693,17 @@ extern "C" int dmla_decode_paged(const void* q, const void* kv_pool, const int32
   hipLaunchKernelGGL(mqa_fwd_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream, p);
   int rc = check_launch("dmla_decode_paged");
   if (rc != DMLA_OK || p.max_splits == 1) return rc;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(B * H)), dim3(kDv / 4), 0, (hipStream_t)stream, p);
-  return check_launch("dmla_decode_paged(combine)");
+  CombineArgs c = {};
+  c.part_o = p.part_o;
+  c.part_lse = p.part_lse;
+  c.seqlens = cache_seqlens;
+  c.o = p.o;
+  c.lse = lse;
+  c.B = (int)B; c.H = (int)H; c.max_splits = p.max_splits; c.d = kDv;
+  c.pages_per_split = p.pages_per_split; c.page_size = kPage; c.max_pages = p.max_pages;
+  c.skip_single = 1;
+  c.po_sb = (int64_t)p.max_splits * H * kDv; c.po_ss = H * kDv; c.po_sh = kDv;
+  c.lse_sb = (int64_t)p.max_splits * H; c.lse_ss = H; c.lse_sh = 1;
+  c.o_sb = o_sb; c.o_sh = o_sh;
+  return launch_lse_combine(c, (hipStream_t)stream, "dmla_decode_paged(combine)");
 }

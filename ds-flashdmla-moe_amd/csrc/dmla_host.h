@@ -22,4 +22,23 @@ inline bool mult8(int64_t s) { return (s % 8) == 0; }
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
+// Split-KV combine (dmla_cache.hip): part_o [.., split, .., d] fp32 partial outputs, each
+// normalised over its split, and part_lse natural-log sums, addressed by element strides.
+// The split count of sequence b is num_splits[b] when given, else derived from seqlens[b] and
+// pages_per_split when given, else max_splits.  skip_single leaves sequences with one split
+// untouched (their rows were written by the producer directly).
+struct CombineArgs {
+  const float* part_o;
+  const float* part_lse;
+  const int32_t* num_splits;
+  const int32_t* seqlens;
+  __bf16* o;
+  float* lse;                 // nullable, [B, H] contiguous
+  int B, H, max_splits, d;
+  int pages_per_split, page_size, max_pages;
+  int skip_single;
+  int64_t po_sb, po_ss, po_sh, lse_sb, lse_ss, lse_sh, o_sb, o_sh;
+};
+int launch_lse_combine(const CombineArgs& a, hipStream_t stream, const char* what);
+
 }  // namespace dmla

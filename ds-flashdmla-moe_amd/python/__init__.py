@@ -10,5 +10,7 @@ from .ops import (  # noqa: F401
     flash_dmla_decode_paged,
     flash_dmla_fwd,
     flash_dmla_fwd_onthefly,
+    flash_dmla_kv_append,
+    flash_dmla_lse_combine,
 )
 from ._lib import DmlaError, DmlaInvalidArgument, DmlaUnsupported  # noqa: F401

@@ -67,6 +67,20 @@ SIGNATURES = {
         + [_i64] * 7  # q_sb q_sh kv_sp kv_ss bt_sb o_sb o_sh
         + [_f32, _ptr, _i64, _ptr],  # scale, workspace, workspace_bytes, stream
     ),
+    "dmla_kv_append": (
+        _int,
+        [_ptr] * 6  # kv_pool, block_table, cache_seqlens, new_lens, new_kv, bad_index_flag
+        + [_i64] * 6  # B, n_new, d, page_size, num_pages, max_pages_per_seq
+        + [_i64] * 5  # kv_sp kv_ss bt_sb nk_sb nk_ss
+        + [_ptr],  # stream
+    ),
+    "dmla_lse_combine": (
+        _int,
+        [_ptr] * 5  # part_o, part_lse, num_splits, o, lse
+        + [_i64] * 4  # B, H, max_splits, d
+        + [_i64] * 8  # po_sb po_ss po_sh lse_sb lse_ss lse_sh o_sb o_sh
+        + [_ptr],  # stream
+    ),
     "dmla_bwd_workspace_bytes": (_i64, [_i64] * 6 + [_int]),  # B H Sq Sk d_qk d_v causal
     "dmla_bwd_cache_latent": (
         _int,

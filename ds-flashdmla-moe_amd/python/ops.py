@@ -191,6 +191,73 @@ def flash_dmla_decode_paged(
     return (o, lse) if return_lse else o
 
 
+def flash_dmla_kv_append(
+    kv_pool: torch.Tensor,
+    block_table: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    new_kv: torch.Tensor,
+    new_lens: Optional[torch.Tensor] = None,
+    check_indices: bool = False,
+) -> None:
+    """Writes new latent rows into the paged cache in place (the producer of decode's pages).
+
+    kv_pool [num_pages, P, d] bf16; block_table [B, max_pages] int32; cache_seqlens [B] int32
+    (rows already cached; not updated); new_kv [B, n_new, d] bf16; new_lens [B] int32 or None.
+    Row t of sequence b lands at position cache_seqlens[b] + t.  Rows whose page slot or page
+    index is out of range are skipped; check_indices=True raises afterwards (one device sync).
+    """
+    _check_bf16("kv_pool", kv_pool, 3)
+    _check_bf16("new_kv", new_kv, 3)
+    for name, t, nd in (("block_table", block_table, 2), ("cache_seqlens", cache_seqlens, 1)):
+        _require(t.dtype == torch.int32 and t.dim() == nd and t.is_cuda, f"{name} must be a {nd}-D int32 GPU tensor")
+    _require(block_table.stride(-1) == 1 and cache_seqlens.is_contiguous(), "index tensors must be contiguous")
+    B, n_new, d = new_kv.shape
+    num_pages, P, dk = kv_pool.shape
+    _require(dk == d, "kv_pool and new_kv row widths differ")
+    _require(block_table.shape[0] == B and cache_seqlens.shape[0] == B, "batch size mismatch")
+    if new_lens is not None:
+        _require(new_lens.dtype == torch.int32 and new_lens.dim() == 1 and new_lens.is_cuda and new_lens.is_contiguous()
+                 and new_lens.shape[0] == B, "new_lens must be a contiguous [B] int32 GPU tensor")
+    flag = torch.zeros(1, dtype=torch.int32, device=kv_pool.device) if check_indices else None
+    _lib.call(
+        "dmla_kv_append",
+        _ptr(kv_pool), _ptr(block_table), _ptr(cache_seqlens), _ptr(new_lens), _ptr(new_kv), _ptr(flag),
+        B, n_new, d, P, num_pages, block_table.shape[1],
+        kv_pool.stride(0), kv_pool.stride(1), block_table.stride(0), new_kv.stride(0), new_kv.stride(1),
+        _stream(kv_pool),
+    )
+    if check_indices:
+        _require(int(flag.item()) == 0, "kv append: a row's page slot or page index was out of range (row skipped)")
+
+
+def flash_dmla_lse_combine(
+    part_o: torch.Tensor,
+    part_lse: torch.Tensor,
+    num_splits: Optional[torch.Tensor] = None,
+    return_lse: bool = False,
+):
+    """Merges split-KV partials: part_o [B, S, H, d] fp32 (each normalised over its split),
+    part_lse [B, S, H] fp32 natural log, num_splits [B] int32 or None (all S).  Returns
+    o [B, H, d] bf16 (and lse [B, H] fp32 with return_lse)."""
+    _require(part_o.dtype == torch.float32 and part_o.is_cuda and part_o.dim() == 4 and part_o.stride(-1) == 1,
+             "part_o must be a [B, S, H, d] float32 GPU tensor, contiguous in d")
+    B, S, H, d = part_o.shape
+    _require(part_lse.dtype == torch.float32 and part_lse.is_cuda and tuple(part_lse.shape) == (B, S, H),
+             "part_lse must be a [B, S, H] float32 GPU tensor")
+    if num_splits is not None:
+        _require(num_splits.dtype == torch.int32 and num_splits.is_cuda and num_splits.is_contiguous()
+                 and tuple(num_splits.shape) == (B,), "num_splits must be a contiguous [B] int32 GPU tensor")
+    o = torch.empty((B, H, d), dtype=torch.bfloat16, device=part_o.device)
+    lse = torch.empty((B, H), dtype=torch.float32, device=part_o.device) if return_lse else None
+    _lib.call(
+        "dmla_lse_combine",
+        _ptr(part_o), _ptr(part_lse), _ptr(num_splits), _ptr(o), _ptr(lse), B, H, S, d,
+        part_o.stride(0), part_o.stride(1), part_o.stride(2), part_lse.stride(0), part_lse.stride(1),
+        part_lse.stride(2), o.stride(0), o.stride(1), _stream(part_o),
+    )
+    return (o, lse) if return_lse else o
+
+
 class FlashDMLACacheLatent(torch.autograd.Function):
     """o = FlashDMLACacheLatent.apply(q, k_lat, d_v, softmax_scale, causal).
 

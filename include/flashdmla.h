@@ -119,6 +119,48 @@ int dmla_decode_paged(const void* q, const void* kv_pool, const int32_t* block_t
                       dmla_stream_t stream);
 
 /*
+ * Paged latent-cache append: writes new rows into the pages the decode reads.
+ * No reference counterpart (the reference has no paged cache); it is the producer side of
+ * dmla_decode_paged's block-table gather.
+ *
+ *   kv_pool      [num_pages, page_size, d] bf16  strides (kv_sp, kv_ss); written in place
+ *   block_table  [B, max_pages_per_seq]    int32 row stride bt_sb
+ *   cache_seqlens[B]                       int32 tokens already cached (not updated here)
+ *   new_lens     [B]                       int32 rows to append per sequence (<= n_new); may be NULL
+ *   new_kv       [B, n_new, d]             bf16  strides (nk_sb, nk_ss)
+ *   bad_index_flag                         int32 device word; may be NULL
+ *
+ * Row t < new_lens[b] of sequence b goes to position p = cache_seqlens[b] + t: page
+ * block_table[b, p / page_size], row p % page_size.  A row whose page slot is past
+ * max_pages_per_seq or whose page index is outside [0, num_pages) is not written, and
+ * *bad_index_flag is set to 1 (the caller clears it beforehand).  d must be a multiple of 8.
+ */
+int dmla_kv_append(void* kv_pool, const int32_t* block_table, const int32_t* cache_seqlens,
+                   const int32_t* new_lens, const void* new_kv, int32_t* bad_index_flag, int64_t B,
+                   int64_t n_new, int64_t d, int64_t page_size, int64_t num_pages,
+                   int64_t max_pages_per_seq, int64_t kv_sp, int64_t kv_ss, int64_t bt_sb,
+                   int64_t nk_sb, int64_t nk_ss, dmla_stream_t stream);
+
+/*
+ * Split-KV log-sum-exp combine, the last step of split decoding, as a standalone op.
+ * No reference counterpart; dmla_decode_paged runs the same kernel on its own partials.
+ *
+ *   part_o   [B, S, H, d] fp32, element strides (po_sb, po_ss, po_sh), last dim contiguous;
+ *            each split's output normalised over that split's keys
+ *   part_lse [B, S, H]    fp32, strides (lse_sb, lse_ss, lse_sh), natural log (-inf: empty)
+ *   num_splits [B]        int32 splits used per sequence (<= S); NULL = all S
+ *   o        [B, H, d]    bf16, strides (o_sb, o_sh)
+ *   lse      [B, H]       fp32 contiguous; may be NULL
+ *
+ *   o = sum_s w_s o_s / sum_s w_s with w_s = exp(lse_s - max_s lse_s), lse = max + log(sum w);
+ *   a sequence whose splits all have lse = -inf gets o = 0 and lse = -inf.  d % 4 == 0.
+ */
+int dmla_lse_combine(const float* part_o, const float* part_lse, const int32_t* num_splits, void* o,
+                     float* lse, int64_t B, int64_t H, int64_t max_splits, int64_t d, int64_t po_sb,
+                     int64_t po_ss, int64_t po_sh, int64_t lse_sb, int64_t lse_ss, int64_t lse_sh,
+                     int64_t o_sb, int64_t o_sh, dmla_stream_t stream);
+
+/*
  * Cache-latent DMLA backward from the forward's saved statistics.
  * Replaces: fa2_backward (csrc/attention/fa2_bwd.cu:319-356, math of :198-310) specialised
  * to the cache-latent mode of README.md:12,15 -- the role of the absent

@@ -22,6 +22,8 @@ whose math this module restates in PyTorch eager (fp32 by default, fp64 for pinn
     (README.md:12) instead of recomputed                               -> dmla_bwd_cache_latent
   * paged decode (no reference counterpart): contiguous attention over the
     tokens gathered through the block table                           -> dmla_decode_paged
+  * the paged-cache append that produces those pages and the split-KV LSE combine (no
+    reference counterparts)                                           -> kv_append, lse_combine
 
 Conventions the reference leaves open, fixed here and in the kernels alike:
   * causal: key j is masked when j > i + (Sk - Sq) (j > i for Sq == Sk);
@@ -175,6 +177,43 @@ def dmla_decode_paged(q: Tensor, kv_pool: Tensor, block_table: Tensor, cache_seq
         outs.append(o.squeeze(1))
         lses.append((m + torch.log(l)).squeeze(1))
     return torch.stack(outs), torch.stack(lses)
+
+
+def kv_append(kv_pool: Tensor, block_table: Tensor, cache_seqlens: Tensor, new_kv: Tensor,
+              new_lens: Optional[Tensor] = None) -> Tensor:
+    """Paged KV-cache append (no reference counterpart; the producer side of gather_pages).
+
+    Token t of sequence b's new rows (t < new_lens[b], default all) lands at position
+    cache_seqlens[b] + t: page block_table[b, pos // P], row pos % P.  Returns the new pool.
+    """
+    out = kv_pool.clone()
+    page_size = kv_pool.shape[1]
+    for b in range(new_kv.shape[0]):
+        n = new_kv.shape[1] if new_lens is None else int(new_lens[b])
+        for t in range(n):
+            pos = int(cache_seqlens[b]) + t
+            out[int(block_table[b, pos // page_size]), pos % page_size] = new_kv[b, t]
+    return out
+
+
+def lse_combine(part_o: Tensor, part_lse: Tensor, num_splits: Optional[Tensor] = None,
+                dtype: torch.dtype = torch.float32) -> Tuple[Tensor, Tensor]:
+    """Merges split-KV partials: part_o [B, S, H, D] (each normalised over its split's keys),
+    part_lse [B, S, H] natural log.  o = sum_s w_s o_s / sum_s w_s with w_s = exp(lse_s - max),
+    lse = max + log(sum_s w_s); splits >= num_splits[b] are ignored; no finite lse -> o = 0,
+    lse = -inf.  The combine of split-KV decoding (no reference counterpart)."""
+    B, S = part_o.shape[0], part_o.shape[1]
+    po, pl = part_o.to(dtype), part_lse.to(dtype)
+    if num_splits is not None:
+        valid = torch.arange(S).view(1, S, 1) < num_splits.view(B, 1, 1).to(torch.long)
+        pl = torch.where(valid, pl, torch.full_like(pl, float("-inf")))
+    mx = pl.amax(dim=1)
+    ref = torch.where(torch.isfinite(mx), mx, torch.zeros_like(mx))
+    w = torch.exp(pl - ref.unsqueeze(1))
+    wsum = w.sum(dim=1)
+    o = (w.unsqueeze(-1) * torch.nan_to_num(po)).sum(dim=1) / torch.where(wsum > 0, wsum, torch.ones_like(wsum)).unsqueeze(-1)
+    lse = torch.where(wsum > 0, ref + torch.log(torch.where(wsum > 0, wsum, torch.ones_like(wsum))), mx)
+    return o, lse
 
 
 def dmla_bwd_cache_latent(q: Tensor, k_lat: Tensor, o: Tensor, do: Tensor, m: Tensor, l: Tensor,

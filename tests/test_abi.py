@@ -143,3 +143,32 @@ def test_bwd_python_wrapper_rejects_cpu_tensors():
     m = torch.zeros(1, 2, 4)
     with pytest.raises(ValueError, match="GPU tensor"):
         ops.flash_dmla_bwd(q, k, o, o, m, m)
+
+
+def test_kv_append_and_combine_argument_errors():
+    lib = _lib.lib()
+    P = ctypes.c_void_p
+
+    def append(**kw):
+        a = dict(pool=1 << 20, bt=1 << 20, sl=1 << 20, new=1 << 20, B=2, n=3, d=576, ps=64, npg=10, mp=4,
+                 kv_sp=64 * 576, kv_ss=576, bt_sb=4)
+        a.update(kw)
+        return lib.dmla_kv_append(P(a["pool"]), P(a["bt"]), P(a["sl"]), None, P(a["new"]), None, a["B"], a["n"],
+                                  a["d"], a["ps"], a["npg"], a["mp"], a["kv_sp"], a["kv_ss"], a["bt_sb"],
+                                  3 * 576, 576, None)
+    assert append(pool=None) == _lib.DMLA_ERR_INVALID_ARG
+    assert append(d=12) == _lib.DMLA_ERR_UNSUPPORTED
+    assert append(kv_ss=8) == _lib.DMLA_ERR_INVALID_ARG           # row stride below d
+    assert append(bt_sb=2) == _lib.DMLA_ERR_INVALID_ARG           # table stride below max pages
+    assert append(new=(1 << 20) + 8) == _lib.DMLA_ERR_INVALID_ARG  # misaligned
+    assert append(n=0) == _lib.DMLA_OK and append(B=0) == _lib.DMLA_OK
+
+    def combine(**kw):
+        a = dict(po=1 << 20, pl=1 << 20, o=1 << 20, B=2, H=4, S=3, d=512)
+        a.update(kw)
+        return lib.dmla_lse_combine(P(a["po"]), P(a["pl"]), None, P(a["o"]), None, a["B"], a["H"], a["S"], a["d"],
+                                    3 * 4 * 512, 4 * 512, 512, 12, 4, 1, 4 * 512, 512, None)
+    assert combine(po=None) == _lib.DMLA_ERR_INVALID_ARG
+    assert combine(S=0) == _lib.DMLA_ERR_INVALID_ARG
+    assert combine(d=6) == _lib.DMLA_ERR_UNSUPPORTED
+    assert combine(B=0) == _lib.DMLA_OK

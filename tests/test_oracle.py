@@ -228,3 +228,56 @@ def test_planted_forward_mistakes_are_caught(mistake):
         m = m * 8.0
     same = (np.allclose(o.numpy(), g["o"][0], atol=1e-5) and np.allclose(m.numpy(), g["m"][0], atol=1e-5))
     assert not same, f"golden forward failed to catch the planted mistake {mistake}"
+
+
+# ---------------------------------------------------------------- paged append and combine
+def test_kv_append_round_trips_through_gather():
+    g = torch.Generator().manual_seed(41)
+    P, D, n_pages = 8, 16, 12
+    pool = torch.randn(n_pages, P, D, generator=g)
+    table = torch.randperm(n_pages, generator=g)[:12].view(2, 6)   # disjoint pages per sequence
+    lens = torch.tensor([5, 13])
+    new = torch.randn(2, 11, D, generator=g)
+    new_lens = torch.tensor([11, 3])
+    out = R.kv_append(pool, table, lens, new, new_lens)
+    for b in range(2):
+        before = R.gather_pages(pool, table[b], int(lens[b]), P)
+        after = R.gather_pages(out, table[b], int(lens[b] + new_lens[b]), P)
+        assert torch.equal(after, torch.cat([before, new[b, : int(new_lens[b])]]))
+    # rows outside the appended positions are untouched
+    touched = torch.zeros(n_pages, P, dtype=torch.bool)
+    for b in range(2):
+        for t in range(int(new_lens[b])):
+            pos = int(lens[b]) + t
+            touched[int(table[b, pos // P]), pos % P] = True
+    assert torch.equal(out[~touched], pool[~touched])
+
+
+def test_lse_combine_of_key_splits_is_full_attention():
+    g = torch.Generator().manual_seed(43)
+    H, N, D, DV = 3, 50, 16, 8
+    q = torch.randn(1, H, 1, D, generator=g, dtype=torch.float64)
+    k = torch.randn(1, N, D, generator=g, dtype=torch.float64)
+    cuts = [0, 7, 7, 30, N]   # includes an empty split
+    parts_o, parts_l = [], []
+    for a, b in zip(cuts[:-1], cuts[1:]):
+        if b > a:
+            o, m, l = R.attention_exact(q[0], k[:, a:b], k[:, a:b, :DV], 0.3, False)
+            parts_o.append(o[:, 0])
+            parts_l.append((m + torch.log(l))[:, 0])
+        else:
+            parts_o.append(torch.full((H, DV), float("nan"), dtype=torch.float64))
+            parts_l.append(torch.full((H,), float("-inf"), dtype=torch.float64))
+    po = torch.stack(parts_o).unsqueeze(0)
+    pl = torch.stack(parts_l).unsqueeze(0)
+    o, lse = R.lse_combine(po, pl, dtype=torch.float64)
+    o_ref, m_ref, l_ref = R.attention_exact(q[0], k, k[..., :DV], 0.3, False)
+    torch.testing.assert_close(o[0], o_ref[:, 0], atol=1e-12, rtol=1e-12)
+    torch.testing.assert_close(lse[0], (m_ref + torch.log(l_ref))[:, 0], atol=1e-12, rtol=1e-12)
+    # num_splits drops the trailing splits: the combine of the first two equals attention over keys 0..6
+    o2, _ = R.lse_combine(po, pl, torch.tensor([2]), dtype=torch.float64)
+    o_pre, _, _ = R.attention_exact(q[0], k[:, :7], k[:, :7, :DV], 0.3, False)
+    torch.testing.assert_close(o2[0], o_pre[:, 0], atol=1e-12, rtol=1e-12)
+    # no finite lse -> o = 0, lse = -inf
+    o3, l3 = R.lse_combine(po[:, 1:2], pl[:, 1:2], dtype=torch.float64)
+    assert torch.all(o3 == 0) and torch.all(torch.isneginf(l3))
