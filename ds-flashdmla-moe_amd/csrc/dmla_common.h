@@ -79,6 +79,22 @@ __device__ __forceinline__ void dma16(const void* sbase, unsigned voff, unsigned
                : "s"(sl), "v"(voff), "s"(reinterpret_cast<const void*>(sb))
                : "memory", "m0");
 }
+// The copy without a compiler memory barrier, so the scheduler may move LDS reads across it
+// (e.g. the next operand reads of an MFMA loop).  The copy overwrites LDS that this wave read
+// as MFMA operands; d0..d3 are results of MFMAs that consumed every one of those reads, and as
+// asm inputs they order the copy after the reads have completed without keeping the operand
+// registers alive.  The caller guarantees that no other wave still reads the destination.
+__device__ __forceinline__ void dma16_after(const void* sbase, unsigned voff, unsigned lds_addr, const f32x4& d0,
+                                            const f32x4& d1, const f32x4& d2, const f32x4& d3) {
+  const uint64_t base = reinterpret_cast<uint64_t>(sbase);
+  const uint64_t sb = ((uint64_t)__builtin_amdgcn_readfirstlane((unsigned)(base >> 32)) << 32) |
+                      (unsigned)__builtin_amdgcn_readfirstlane((unsigned)base);
+  const unsigned sl = __builtin_amdgcn_readfirstlane(lds_addr);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(sl), "v"(voff), "s"(reinterpret_cast<const void*>(sb)), "v"(d0), "v"(d1), "v"(d2), "v"(d3)
+               : "m0");
+}
 // Same copy with a full 64-bit global address per lane (rows of one tile that are far apart,
 // e.g. query rows of different heads).
 __device__ __forceinline__ void dma16_addr(const void* gaddr, unsigned lds_addr) {

@@ -27,6 +27,8 @@
 //  * Softmax in the exp2 domain against a per-row reference max fixed at the first tile: p
 //    stays below 2^kHeadroom, so O is never rescaled.  Scores climbing past that headroom
 //    trigger a recomputation of the row tile from a higher reference.
+#include <type_traits>
+
 #include "dmla_common.h"
 #include "dmla_host.h"
 
@@ -158,9 +160,8 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
 #pragma unroll
     for (int c = 0; c < kKcHalf; ++c) qreg[qg][c] = *reinterpret_cast<const bf16x8*>(qrow + 32 * c);
   }
-  // Q must have landed before the first tile copy is issued: the compiler does not count the
-  // (inline assembly) copies, so a later wait of its own for Q would drain them too.
-  wait_vmem();
+  // No wait for Q here: the first tile copies go out behind it and one wait_vmem covers both
+  // (vmcnt retires loads in issue order, so the compiler's own counts for Q stay conservative).
 
   // ---- tile staging ----------------------------------------------------------------------
   // Wave w copies chunk group w -- the output columns it alone reads in PV -- in 4 copies of 8
@@ -173,7 +174,10 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   const int row_stride_bytes = (int)(p.k_ss * 2);
   // Row 8r + l/8 of a copy has swizzle swz(8 (r & 1) + l/8): two column variants per lane.
   const int dma_lrow = lane >> 3;
-  const unsigned dma_col[2] = {16u * ((lane & 7) ^ swz(dma_lrow)), 16u * ((lane & 7) ^ swz(8 + dma_lrow))};
+  // (Two scalars and an xor, not a two-element array: an array indexed by the runtime rope row
+  // would be placed in LDS by the compiler, one ds_read and a full lgkmcnt wait per copy.)
+  const unsigned dma_col0 = 16u * ((lane & 7) ^ swz(dma_lrow));
+  const unsigned dma_col_x = dma_col0 ^ (16u * ((lane & 7) ^ swz(8 + dma_lrow)));
   const unsigned dma_lane = (unsigned)(dma_lrow * row_stride_bytes);
   const int dma_rope_r = wave & 3;   // rope copy of waves 0..3: rows 8w .. 8w+7
   const int ncopies = wave < 4 ? 5 : 4;
@@ -197,20 +201,25 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   auto slot_addr = [&](int tile) { return lds_base + ((tile - tile_begin + kRing) % kRing) * kTileBytes; };
   // Copy k (0..ncopies-1) of this wave; rows past the valid range re-read row 0 of the tile
   // (finite data, masked later).
-  auto copy_part = [&](int k, const char* src, int valid_rows, unsigned dst) {
+  f32x4 oacc[kDbWave][4];   // O^T[64 wave + 16 d + 4 g + i][16 qg + l16]
+  auto copy_part = [&](int k, const char* src, int valid_rows, unsigned dst, auto after_tag) {
     const int r = k < 4 ? k : dma_rope_r;
-    const unsigned col = (r & 1) ? dma_col[1] : dma_col[0];
+    const unsigned col = dma_col0 ^ ((r & 1) ? dma_col_x : 0u);
     const unsigned off = 8 * r + dma_lrow < valid_rows ? dma_lane + (unsigned)(8 * r * row_stride_bytes) + col : col;
-    if (k < 4) dma16(src + wave * 128, off, dst + wave * kGroupBytes + k * 1024);
-    else dma16(src + 8 * 128, off, dst + 8 * kGroupBytes + dma_rope_r * 1024);
+    const void* gsrc = k < 4 ? (const void*)(src + wave * 128) : (const void*)(src + 8 * 128);
+    const unsigned ldst = k < 4 ? dst + wave * kGroupBytes + k * 1024 : dst + 8 * kGroupBytes + dma_rope_r * 1024;
+    // After PV: oacc[d][0] consumed the V read of column block d (see dma16_after).
+    if constexpr (decltype(after_tag)::value) dma16_after(gsrc, off, ldst, oacc[0][0], oacc[1][0], oacc[2][0], oacc[3][0]);
+    else dma16(gsrc, off, ldst);
   };
+  using Plain = std::integral_constant<bool, false>;
   auto stage = [&](int tile, int slot_tile) {
     int valid_rows;
     const char* src = tile_src(tile, valid_rows);
     const unsigned dst = slot_addr(slot_tile);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) copy_part(k, src, valid_rows, dst);
-    if (ncopies > 4) copy_part(4, src, valid_rows, dst);
+    for (int k = 0; k < 4; ++k) copy_part(k, src, valid_rows, dst, Plain{});
+    if (ncopies > 4) copy_part(4, src, valid_rows, dst, Plain{});
   };
 
   // ---- per-lane LDS byte offsets -----------------------------------------------------------
@@ -236,7 +245,6 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
 
   auto slot_of = [&](int t) { return lds + ((t - tile_begin + kRing) % kRing) * kTileBytes; };
 
-  f32x4 oacc[kDbWave][4];   // O^T[64 wave + 16 d + 4 g + i][16 qg + l16]
   float mref;               // max the accumulators of the own rows are relative to
   float mtrue;              // exact running max of this lane's keys of its own row
   float lsum;               // this lane's partial row sum relative to mref
@@ -261,26 +269,45 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   };
   // Partial S^T[key 16 kh + 4g + i][pair row 16 qg + l16] of tile tq over this wave's dims
   // half; the copies of tile `ctile` into its ring slot are issued between the k-steps.
-  auto qk = [&](int tq, f32x4 (&sacc)[2], int ctile) {
+  // kCopy: 0 for the last two tiles of a work item (there is no tile t+2 to fetch); 1 copies
+  // into a slot nobody has read since the last barrier; 2 refills the slot this wave's PV just
+  // read, ordered after those reads by register dependences (no wait for other LDS reads, so
+  // the K reads can run ahead of it).
+  auto qk = [&](int tq, f32x4 (&sacc)[2], int ctile, auto copy_tag) {
+    constexpr int kCopy = decltype(copy_tag)::value;
     const DMLA_LDS char* tb = slot_of(tq);
-    int valid_rows;
-    const char* src = tile_src(ctile, valid_rows);
-    const unsigned dst = slot_addr(ctile);
+    int valid_rows = 0;
+    const char* src = nullptr;
+    unsigned dst = 0;
+    if constexpr (kCopy) {
+      src = tile_src(ctile, valid_rows);
+      dst = slot_addr(ctile);
+    }
     sacc[0] = sacc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // K operands are read two k-steps ahead of their MFMAs.
+    auto kread = [&](int c) {
+      const int cc = kHalf * kKcHalf + c;
+      return lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(tb + k_off[cc & 1] + (cc >> 1) * kGroupBytes));
+    };
+    bf16x8 kb[3];
+    kb[0] = kread(0);
+    kb[1] = kread(1);
 #pragma unroll
     for (int c = 0; c < kKcHalf; ++c) {
-      constexpr int c0 = kHalf * kKcHalf;
-      const int cc = c0 + c;
-      const int off = k_off[cc & 1] + (cc >> 1) * kGroupBytes;
-      const bf16x8 a = lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(tb + off));
+      if (c + 2 < kKcHalf) kb[(c + 2) % 3] = kread(c + 2);
+      const bf16x8 a = kb[c % 3];
       sacc[0] = mfma_bf16(a, qreg[0][c], sacc[0]);
       sacc[1] = mfma_bf16(a, qreg[1][c], sacc[1]);
-      // The copies refill the slot this wave's PV just read: its LDS reads must be complete.
-      if (c == 0) __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-      if (c < 4) copy_part(c, src, valid_rows, dst);
-      if (c == 4 && ncopies > 4) copy_part(4, src, valid_rows, dst);
+      if constexpr (kCopy != 0) {
+        using Tag = std::integral_constant<bool, kCopy == 2>;
+        if (c < 4) copy_part(c, src, valid_rows, dst, Tag{});
+        if (c == 4 && ncopies > 4) copy_part(4, src, valid_rows, dst, Tag{});
+      }
     }
   };
+  using CopyOn = std::integral_constant<int, 1>;
+  using CopyOff = std::integral_constant<int, 0>;
+  using CopyAfterPv = std::integral_constant<int, 2>;
   auto post_partial = [&](int tq, const f32x4 (&sacc)[2]) {
     *reinterpret_cast<DMLA_LDS f32x4*>(xbuf + (tq & 1) * kXBytes + x_post) = sacc[1 - kHalf];
   };
@@ -308,7 +335,6 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   lsum = 0.f;
   mref = kNegInf;
   bool overflow = false;
-  int ovf_any = 0;
   if (tile_begin < tile_end) {
     if constexpr (kExact) {
       // Scores-only pass for the exact row max (rows without any key keep -inf).
@@ -317,7 +343,8 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
       for (int t = tile_begin; t < tile_end; ++t) {
         wait_vmem();
         __syncthreads();
-        qk(t, sacc, t + 1);
+        if (t + 1 < tile_end) qk(t, sacc, t + 1, CopyOn{});
+        else qk(t, sacc, t + 1, CopyOff{});
         post_partial(t, sacc);
         __syncthreads();
         float sr[4];
@@ -336,10 +363,10 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     stage(tile_begin, tile_begin - 1);
     stage(tile_begin, tile_begin);
     *reinterpret_cast<DMLA_LDS bf16x4*>(pbuf + ((tile_begin - 1) & 1) * kPBytes + p_post) = bf16x4{0.f, 0.f, 0.f, 0.f};
-    flags[((tile_begin - 1) & 1) * kWaves + wave] = 0;
     wait_vmem();
     __syncthreads();
-    qk(tile_begin, sacc, tile_begin + 1);
+    if (tile_begin + 1 < tile_end) qk(tile_begin, sacc, tile_begin + 1, CopyOn{});
+    else qk(tile_begin, sacc, tile_begin + 1, CopyOff{});
     post_partial(tile_begin, sacc);
     if constexpr (!kExact) {
       __syncthreads();
@@ -354,21 +381,19 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     // Iteration t: PV(t-1) and the partial scores of tile t+1 on the matrix cores with
     // softmax(t) in between, then P(t) and the partials of t+1 are posted.  One barrier per
     // tile.  Ring: PV reads slot(t-1), QK reads slot(t+1), slot(t) waits for PV(t), and each
-    // wave refills its own part of slot(t-1) with tile t+2 after its PV.
-    for (int t = tile_begin; t < tile_end; ++t) {
+    // wave refills its own part of slot(t-1) with tile t+2 after its PV.  kKind 0 is the
+    // steady state; the last two iterations are peeled: kKind 1 fetches no tile t+2 and
+    // kKind 2 (the last tile) computes no scores for a tile t+1.  An overflow of the reference
+    // max is only recorded per lane here and acted on once, after the last tile: inputs that
+    // trigger it are rare, and a per-tile exchange of flags would cost every tile LDS traffic.
+    auto iteration = [&](int t, auto kind_tag) {
+      constexpr int kKind = decltype(kind_tag)::value;
       wait_vmem();       // this wave's copies of tile t+1 have landed
-      __syncthreads();   // partials(t), P(t-1), flags posted; tile t+1 complete
-      // Overflow flags of tile t-1 are read now but acted on at the end of the iteration, so
-      // their LDS round trip stays off the critical path (the extra tile's work is discarded).
-      // Double-buffered by tile parity: every wave reads the same values before anyone writes.
-      i32x4 f0 = {0, 0, 0, 0}, f1 = {0, 0, 0, 0};
-      if constexpr (!kExact) {
-        f0 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags + ((t - 1) & 1) * kWaves);
-        f1 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags + ((t - 1) & 1) * kWaves + 4);
-      }
+      __syncthreads();   // partials(t) and P(t-1) posted; tile t+1 complete
       const f32x4 s = take_scores(t, sacc);
       pv(t - 1);
-      qk(t + 1, sacc, t + 2);
+      if constexpr (kKind == 0) qk(t + 1, sacc, t + 2, CopyAfterPv{});
+      if constexpr (kKind == 1) qk(t + 1, sacc, t + 2, CopyOff{});
 
       // ---- softmax of the own 16 rows x 16 keys (exp2 domain) ------------------------------
       float sr[4];
@@ -385,23 +410,22 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
         pk[j] = (bf16)pj;
       }
       *reinterpret_cast<DMLA_LDS bf16x4*>(pbuf + (t & 1) * kPBytes + p_post) = pk;
-      post_partial(t + 1, sacc);
-      iteration_schedule();
-      if constexpr (!kExact) {
-        ovf_any = (f0[0] | f0[1] | f0[2] | f0[3]) | (f1[0] | f1[1] | f1[2] | f1[3]);
-        flags[(t & 1) * kWaves + wave] = __any(overflow) ? 1 : 0;
-        if (ovf_any != 0) break;
+      if constexpr (kKind != 2) {
+        post_partial(t + 1, sacc);
+        iteration_schedule();
       }
-    }
+    };
+    int t = tile_begin;
+    for (; t + 2 < tile_end; ++t) iteration(t, std::integral_constant<int, 0>{});
+    if (t + 1 < tile_end) iteration(t++, std::integral_constant<int, 1>{});
+    iteration(t, std::integral_constant<int, 2>{});
+    if constexpr (!kExact) flags[wave] = __any(overflow) ? 1 : 0;
     wait_vmem();
-    __syncthreads();     // P(end-1) and the flags of the last tile posted (or a break)
+    __syncthreads();     // P(end-1) and the overflow flags posted
     if constexpr (!kExact) {
-      if (ovf_any == 0) {  // the last tile's flags were never read inside the loop
-        const i32x4 f0 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags + ((tile_end - 1) & 1) * kWaves);
-        const i32x4 f1 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags + ((tile_end - 1) & 1) * kWaves + 4);
-        ovf_any = (f0[0] | f0[1] | f0[2] | f0[3]) | (f1[0] | f1[1] | f1[2] | f1[3]);
-      }
-      if (ovf_any != 0) {
+      const i32x4 f0 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags);
+      const i32x4 f1 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags + 4);
+      if (((f0[0] | f0[1] | f0[2] | f0[3]) | (f1[0] | f1[1] | f1[2] | f1[3])) != 0) {
         mqa_fwd_exact<kDecode, kHalf>(params, wk, lds, wave, lane);
         return;
       }
