@@ -252,20 +252,28 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   const float scale_log2 = p.scale_log2;
 
   // PV of tile tp for this wave's 64 columns and all 64 rows.
-  auto pv = [&](int tp) {
+  // The V operands of a tile are read one iteration ahead of its PV (vload), off the burst
+  // of P reads that follows each barrier; a slot's data is complete from the barrier after
+  // its copies landed until this wave's next copies into it.
+  bf16x8 vpre[kDbWave];
+  auto vload = [&](int tp) {
     const DMLA_LDS char* tb = slot_of(tp);
+#pragma unroll
+    for (int d = 0; d < kDbWave; ++d) {
+      const bf16x4 v0 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tb + v_off[d]));
+      const bf16x4 v1 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tb + v_off[d] + 16 * 128));
+      vpre[d] = concat(v0, v1);
+    }
+  };
+  auto pv = [&](int tp) {
     const DMLA_LDS char* pb = pbuf + (tp & 1) * kPBytes;
     bf16x8 pall[4];
 #pragma unroll
     for (int qg = 0; qg < 4; ++qg) pall[qg] = *reinterpret_cast<const DMLA_LDS bf16x8*>(pb + qg * 1024 + lane * 16);
 #pragma unroll
-    for (int d = 0; d < kDbWave; ++d) {
-      const bf16x4 v0 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tb + v_off[d]));
-      const bf16x4 v1 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tb + v_off[d] + 16 * 128));
-      const bf16x8 a = concat(v0, v1);
+    for (int d = 0; d < kDbWave; ++d)
 #pragma unroll
-      for (int qg = 0; qg < 4; ++qg) oacc[d][qg] = mfma_bf16(a, pall[qg], oacc[d][qg]);
-    }
+      for (int qg = 0; qg < 4; ++qg) oacc[d][qg] = mfma_bf16(vpre[d], pall[qg], oacc[d][qg]);
   };
   // Partial S^T[key 16 kh + 4g + i][pair row 16 qg + l16] of tile tq over this wave's dims
   // half; the copies of tile `ctile` into its ring slot are issued between the k-steps.
@@ -377,6 +385,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     } else {
       mref = mref_init;
     }
+    vload(tile_begin - 1);
 
     // Iteration t: PV(t-1) and the partial scores of tile t+1 on the matrix cores with
     // softmax(t) in between, then P(t) and the partials of t+1 are posted.  One barrier per
@@ -394,6 +403,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
       pv(t - 1);
       if constexpr (kKind == 0) qk(t + 1, sacc, t + 2, CopyAfterPv{});
       if constexpr (kKind == 1) qk(t + 1, sacc, t + 2, CopyOff{});
+      vload(t);
 
       // ---- softmax of the own 16 rows x 16 keys (exp2 domain) ------------------------------
       float sr[4];
@@ -466,22 +476,42 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   }
   __syncthreads();
   const int col = 64 * wave + 4 * g;
+  if constexpr (!kDecode) {
+    // O goes out as whole 1 KB rows: each wave writes its 64 x 64 block (scaled, bf16) into
+    // the free ring slots as [row][512] with the 16-byte chunks of row r xor-swizzled by r % 16
+    // (two-way bank conflicts at most), then stores 8 rows with 16 contiguous bytes per lane.
+    DMLA_LDS char* ost = lds;
 #pragma unroll
-  for (int qg = 0; qg < 4; ++qg) {
-    const int r = row0 + 16 * qg + l16;
-    if (r >= nrows) continue;
-    const float inv = inv_l[16 * qg + l16];
-    if constexpr (!kDecode) {
-      const int pos = r / p.H, head = r - pos * p.H;
-      bf16* orp = p.o + b * p.o_sb + head * p.o_sh + pos * p.o_ss + col;
+    for (int qg = 0; qg < 4; ++qg) {
+      const int rl = 16 * qg + l16;
+      const float inv = inv_l[rl];
 #pragma unroll
       for (int d = 0; d < kDbWave; ++d) {
         const f32x4 v = oacc[d][qg] * inv;
         bf16x4 w;
         w[0] = (bf16)v[0]; w[1] = (bf16)v[1]; w[2] = (bf16)v[2]; w[3] = (bf16)v[3];
-        *reinterpret_cast<bf16x4*>(orp + 16 * d) = w;
+        const int chunk = (8 * wave + 2 * d + (g >> 1)) ^ (rl & 15);
+        *reinterpret_cast<DMLA_LDS bf16x4*>(ost + rl * 1024 + chunk * 16 + (g & 1) * 8) = w;
       }
-    } else if (wk.nsplit == 1) {
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int rl = 8 * wave + k;
+      const int r = row0 + rl;
+      if (r >= nrows) break;
+      const bf16x8 v = *reinterpret_cast<const DMLA_LDS bf16x8*>(ost + rl * 1024 + (lane ^ (rl & 15)) * 16);
+      const int pos = r / p.H, head = r - pos * p.H;
+      *reinterpret_cast<bf16x8*>(p.o + b * p.o_sb + head * p.o_sh + pos * p.o_ss + 8 * lane) = v;
+    }
+    return;
+  }
+#pragma unroll
+  for (int qg = 0; qg < 4; ++qg) {
+    const int r = row0 + 16 * qg + l16;
+    if (r >= nrows) continue;
+    const float inv = inv_l[16 * qg + l16];
+    if (wk.nsplit == 1) {
       bf16* orp = p.o + b * p.o_sb + r * p.o_sh + col;
 #pragma unroll
       for (int d = 0; d < kDbWave; ++d) {
