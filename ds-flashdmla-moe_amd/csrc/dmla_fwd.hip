@@ -55,6 +55,14 @@ constexpr int kPOffset = kXOffset + 2 * kXBytes;
 constexpr int kRowOffset = kPOffset + 2 * kPBytes;  // per-row exchange [3][2 key halves][64]
 constexpr int kFlagOffset = kRowOffset + 3 * 2 * kRowsPerWG * 4;
 constexpr int kPageOffset = kFlagOffset + 2 * kWaves * 4;
+// Q staging at the start of a work item: the 64 rows (1152 B each, padded by one 16-byte chunk
+// so that 16 consecutive rows fall into distinct LDS banks) from ring slot 1 on.  Slot 0 takes
+// the first key tile meanwhile; the region reaches 1 KB into partial-score buffer 0, which is
+// first written after Q has been read out.
+constexpr int kQRowBytes = kDqk * 2 + 16;
+constexpr int kQChunks = kRowsPerWG * kQRowBytes / 16;   // 4672 16-byte chunks, 73 per row
+constexpr int kQOffset = kTileBytes;
+static_assert(kQOffset + kRowsPerWG * kQRowBytes <= kXOffset + kXBytes, "Q staging fits before buffer 1");
 constexpr int kLdsBytes = kPageOffset + kMaxSplitPages * 4;
 constexpr float kHeadroom = 32.0f;                  // log2 headroom of p over the reference max
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
@@ -143,25 +151,9 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   const int own_lim = own_row < nrows ? limit_of(own_row) : -1;
 
   // ---- Q: the pair's 32 rows, this wave's dims half, as MFMA B operand --------------------
-  // lane holds Q[row 32 pair + 16 qg + l16][288 kHalf + 32 c + 8 g .. +7]
+  // lane holds Q[row 32 pair + 16 qg + l16][288 kHalf + 32 c + 8 g .. +7]; loaded through LDS
+  // below (one copy per workgroup, whole rows per copy instruction).
   bf16x8 qreg[2][kKcHalf];
-#pragma unroll
-  for (int qg = 0; qg < 2; ++qg) {
-    const int rq = row0 + 32 * pair + 16 * qg + l16;
-    const int r = rq < nrows ? rq : 0;
-    const bf16* qrow;
-    if constexpr (!kDecode) {
-      const int pos = r / p.H, head = r - pos * p.H;
-      qrow = p.q + b * p.q_sb + head * p.q_sh + pos * p.q_ss;
-    } else {
-      qrow = p.q + b * p.q_sb + r * p.q_sh;
-    }
-    qrow += kHalf * (kDqk / 2) + 8 * g;
-#pragma unroll
-    for (int c = 0; c < kKcHalf; ++c) qreg[qg][c] = *reinterpret_cast<const bf16x8*>(qrow + 32 * c);
-  }
-  // No wait for Q here: the first tile copies go out behind it and one wait_vmem covers both
-  // (vmcnt retires loads in issue order, so the compiler's own counts for Q stay conservative).
 
   // ---- tile staging ----------------------------------------------------------------------
   // Wave w copies chunk group w -- the output columns it alone reads in PV -- in 4 copies of 8
@@ -343,11 +335,43 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   lsum = 0.f;
   mref = kNegInf;
   bool overflow = false;
+
+  // ---- Q through LDS, with the first key tile in flight beside it ---------------------------
+  // Chunk k of the staging area is 16-byte chunk k % 73 of row k / 73 (chunk 72 is the row's
+  // padding and re-reads chunk 0); rows past the last one re-read row 0 of the item.
+  {
+    const unsigned qbase = lds_base + kQOffset;
+    for (int i = wave; i * 64 < kQChunks; i += kWaves) {
+      const int k = i * 64 + lane;
+      const int rl = k / (kQRowBytes / 16), ch = k - rl * (kQRowBytes / 16);
+      const int rq = row0 + rl;
+      const int r = rq < nrows ? rq : 0;
+      const bf16* qrow;
+      if constexpr (!kDecode) {
+        const int pos = r / p.H, head = r - pos * p.H;
+        qrow = p.q + b * p.q_sb + head * p.q_sh + pos * p.q_ss;
+      } else {
+        qrow = p.q + b * p.q_sb + r * p.q_sh;
+      }
+      dma16_addr(qrow + 8 * (ch < kDqk / 8 ? ch : 0), qbase + i * 1024);
+    }
+  }
+  if (tile_begin < tile_end) stage(tile_begin, tile_begin);
+  wait_vmem();
+  __syncthreads();
+#pragma unroll
+  for (int qg = 0; qg < 2; ++qg)
+#pragma unroll
+    for (int c = 0; c < kKcHalf; ++c)
+      qreg[qg][c] = lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(
+          lds + kQOffset + (32 * pair + 16 * qg + l16) * kQRowBytes + (kHalf * (kDqk / 2) + 32 * c + 8 * g) * 2));
+  __syncthreads();   // Q is read out before the tile copies below reuse its LDS
+
   if (tile_begin < tile_end) {
     if constexpr (kExact) {
-      // Scores-only pass for the exact row max (rows without any key keep -inf).
+      // Scores-only pass for the exact row max (rows without any key keep -inf); slot(t0)
+      // already holds tile t0.
       float mx = kNegInf;
-      stage(tile_begin, tile_begin);
       for (int t = tile_begin; t < tile_end; ++t) {
         wait_vmem();
         __syncthreads();
@@ -364,15 +388,19 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
       __syncthreads();
     }
 
-    // Prologue: slot(t0-1) holds finite data (a copy of t0) and P(t0-1) = 0, so the PV of the
-    // first iteration adds nothing; slot(t0) holds t0; its partial scores are posted and the
-    // copy of t0+1 is in flight.  The fast path's reference max of each row is its max over
-    // tile t0 (every row with any key has one in the first tile of its work item).
-    stage(tile_begin, tile_begin - 1);
-    stage(tile_begin, tile_begin);
+    // Prologue: the V operands of a tile t0-1 are zero and P(t0-1) = 0, so the PV of the first
+    // iteration adds nothing; slot(t0) holds t0 (restaged after the exact path's scores pass);
+    // its partial scores are posted and the copy of t0+1 is in flight.  The fast path's
+    // reference max of each row is its max over tile t0 (every row with any key has one in
+    // the first tile of its work item).
+#pragma unroll
+    for (int d = 0; d < kDbWave; ++d) vpre[d] = bf16x8{};
     *reinterpret_cast<DMLA_LDS bf16x4*>(pbuf + ((tile_begin - 1) & 1) * kPBytes + p_post) = bf16x4{0.f, 0.f, 0.f, 0.f};
-    wait_vmem();
-    __syncthreads();
+    if constexpr (kExact) {
+      stage(tile_begin, tile_begin);
+      wait_vmem();
+      __syncthreads();
+    }
     if (tile_begin + 1 < tile_end) qk(tile_begin, sacc, tile_begin + 1, CopyOn{});
     else qk(tile_begin, sacc, tile_begin + 1, CopyOff{});
     post_partial(tile_begin, sacc);
@@ -385,7 +413,6 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     } else {
       mref = mref_init;
     }
-    vload(tile_begin - 1);
 
     // Iteration t: PV(t-1) and the partial scores of tile t+1 on the matrix cores with
     // softmax(t) in between, then P(t) and the partials of t+1 are posted.  One barrier per
