@@ -12,7 +12,8 @@ namespace dmla {
 // ---- split-KV combine --------------------------------------------------------------------
 // One 128-thread block per (sequence, head); 4 columns per thread and pass.
 //   o = sum_s w_s o_s / sum_s w_s, w_s = exp(lse_s - max_s lse_s), lse = max + log(sum w)
-// over the first n_b splits; no finite lse leaves o = 0 and lse = -inf (max of the inputs).
+// over the first n_b splits; no finite lse leaves o = 0 and lse = -inf (max of the inputs);
+// a NaN lse makes o and lse NaN.
 __global__ void __launch_bounds__(128) lse_combine_kernel(CombineArgs a) {
   const int b = blockIdx.x / a.H, h = blockIdx.x % a.H;
   int n = a.max_splits;
@@ -24,19 +25,34 @@ __global__ void __launch_bounds__(128) lse_combine_kernel(CombineArgs a) {
     n = max(1, (npages + a.pages_per_split - 1) / a.pages_per_split);
   }
   if (a.skip_single && n == 1) return;   // the decode kernel already wrote such rows itself
-  const int64_t lbase = (int64_t)b * a.lse_sb + (int64_t)h * a.lse_sh;
+  const int64_t s0 = a.split_base != nullptr ? (int64_t)a.split_base[b] : 0;
+  const int64_t lbase = (a.split_base != nullptr ? s0 * a.lse_ss : (int64_t)b * a.lse_sb) + (int64_t)h * a.lse_sh;
   float mx = kNegInf;
-  for (int s = 0; s < n; ++s) mx = fmaxf(mx, a.part_lse[lbase + (int64_t)s * a.lse_ss]);
+  bool bad = false;   // a NaN lse (e.g. a split that met an invalid page) poisons the sequence
+  for (int s = 0; s < n; ++s) {
+    const float lv = a.part_lse[lbase + (int64_t)s * a.lse_ss];
+    bad = bad || lv != lv;
+    mx = fmaxf(mx, lv);
+  }
+  if (bad) {
+    const float nanv = __builtin_nanf("");
+    for (int col = 4 * threadIdx.x; col < a.d; col += 4 * blockDim.x) {
+      const bf16 nb = (bf16)nanv;
+      *reinterpret_cast<bf16x4*>(a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + col) = bf16x4{nb, nb, nb, nb};
+    }
+    if (threadIdx.x == 0 && a.lse != nullptr) a.lse[(int64_t)b * a.H + h] = nanv;
+    return;
+  }
   const float mref = mx == kNegInf ? 0.f : mx;
   float wsum = 0.f;
   for (int s = 0; s < n; ++s) wsum += __expf(a.part_lse[lbase + (int64_t)s * a.lse_ss] - mref);
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  const int64_t obase = (int64_t)b * a.po_sb + (int64_t)h * a.po_sh;
+  const int64_t obase = (a.split_base != nullptr ? s0 * a.po_ss : (int64_t)b * a.po_sb) + (int64_t)h * a.po_sh;
   for (int col = 4 * threadIdx.x; col < a.d; col += 4 * blockDim.x) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int s = 0; s < n; ++s) {
       const float lv = a.part_lse[lbase + (int64_t)s * a.lse_ss];
-      if (!(lv > kNegInf)) continue;   // an empty split may hold anything in its o slot
+      if (lv == kNegInf) continue;   // an empty split may hold anything in its o slot
       const float w = __expf(lv - mref);
       acc += w * *reinterpret_cast<const f32x4*>(a.part_o + obase + (int64_t)s * a.po_ss + col);
     }

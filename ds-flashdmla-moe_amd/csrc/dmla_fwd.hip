@@ -104,17 +104,29 @@ struct MqaParams {
   int64_t bt_sb;
   int num_pages;
   int max_pages;
-  int pages_per_split;
-  int max_splits;
   int head_groups;     // ceil(H / 64)
-  int n_units;         // B * max_splits
-  float* part_o;       // [B, max_splits, H, 512] normalised partial outputs
-  float* part_lse;     // [B, max_splits, H]
+  int n_ranges;        // R of the decode plan
+  const int32_t* plan; // decode plan (see decode_plan_kernel)
+  float* part_o;       // [slots, H, 512] normalised partial outputs
+  float* part_lse;     // [slots, H]
 };
 
 struct Work {
-  int b, row0, tile_begin, tile_end, split, nsplit, ctx, page_begin;
+  int b, row0, tile_begin, tile_end, split, nsplit, ctx, page_begin, slot;
 };
+
+// ---- decode plan --------------------------------------------------------------------------
+// The key tiles (32 tokens) of all sequences, in order, are cut into R ranges of T tiles each
+// (T = ceil(total / R)); range r is processed by head_groups workgroups on one XCD, one per
+// group of 64 heads, so every workgroup gets the same number of tiles whatever the context
+// lengths.  A range may span several sequences: each piece is one split of its sequence, and
+// sequences with more than one split are merged by the LSE combine.
+// Layout (int32): header[8] = {B, R, T, total tiles, total splits, 0, 0, 0}, then
+// tile_prefix[B + 1], split_base[B + 1] (first partial slot of each sequence), num_splits[B],
+// range_first_b[R] (the sequence containing the range's first tile).
+constexpr int kPlanHeader = 8;
+constexpr int kMaxSegTiles = 2 * kMaxSplitPages - 2;   // a segment's pages fit the page cache
+__host__ __device__ inline int64_t plan_ints(int64_t B, int64_t R) { return kPlanHeader + 3 * B + 2 + R; }
 
 template <bool kDecode, int kHalf>
 __device__ __noinline__ void mqa_fwd_exact(const MqaParams* params, Work wk, DMLA_LDS char* lds, int wave, int lane);
@@ -497,7 +509,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
       if (wk.nsplit == 1) {
         if (p.lse != nullptr) p.lse[b * p.H + own_row] = lse;
       } else {
-        p.part_lse[((int64_t)b * p.max_splits + wk.split) * p.H + own_row] = lse;
+        p.part_lse[(int64_t)wk.slot * p.H + own_row] = lse;
       }
     }
   }
@@ -549,8 +561,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
         *reinterpret_cast<bf16x4*>(orp + 16 * d) = w;
       }
     } else {
-      const int64_t slot = ((int64_t)b * p.max_splits + wk.split) * p.H + r;
-      float* pp = p.part_o + slot * kDv + col;
+      float* pp = p.part_o + ((int64_t)wk.slot * p.H + r) * kDv + col;
 #pragma unroll
       for (int d = 0; d < kDbWave; ++d) {
         f32x4 v = oacc[d][qg] * inv;
@@ -575,7 +586,7 @@ __device__ __noinline__ void mqa_fwd_exact(const MqaParams* params, Work wk, DML
   wave = uniform(wave);
   wk.b = uniform(wk.b); wk.row0 = uniform(wk.row0); wk.tile_begin = uniform(wk.tile_begin);
   wk.tile_end = uniform(wk.tile_end); wk.split = uniform(wk.split); wk.nsplit = uniform(wk.nsplit);
-  wk.ctx = uniform(wk.ctx); wk.page_begin = uniform(wk.page_begin);
+  wk.ctx = uniform(wk.ctx); wk.page_begin = uniform(wk.page_begin); wk.slot = uniform(wk.slot);
   lds = reinterpret_cast<DMLA_LDS char*>(static_cast<uintptr_t>(uniform((int)lds_addr(lds))));
   __syncthreads();
   mqa_fwd_body<kDecode, kHalf, true>(p, &p, wk, lds, wave, lane);
@@ -603,47 +614,128 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
     wk.tile_begin = 0;
     wk.tile_end = (kend + kTileN - 1) / kTileN;
     wk.nsplit = 1;
+    const MqaParams* params = (const MqaParams*)(__builtin_amdgcn_kernarg_segment_ptr());
+    if (((wave >> 1) & 1) == 0) mqa_fwd_body<kDecode, 0, false>(p, params, wk, lds, wave, lane);
+    else mqa_fwd_body<kDecode, 1, false>(p, params, wk, lds, wave, lane);
   } else {
-    // Id -> (unit = (b, split), head group) with the head groups of one unit 8 ids apart, so
-    // they run on the same XCD and the second read of the unit's pages hits that XCD's L2.
+    // Workgroup -> (range r, head group k) with the head groups of a range 8 ids apart, so
+    // they run on the same XCD and the second read of the range's pages hits that XCD's L2.
     const int id = blockIdx.x;
-    const int hg = (id / 8) % p.head_groups;
-    const int unit = (id / (8 * p.head_groups)) * 8 + id % 8;
-    if (unit >= p.n_units) return;
-    wk.b = unit / p.max_splits;
-    wk.split = unit % p.max_splits;
-    wk.row0 = hg * kRowsPerWG;
-    wk.ctx = min(max(p.seqlens[wk.b], 0), p.max_pages * kPage);
-    const int npages = (wk.ctx + kPage - 1) / kPage;
-    wk.nsplit = max(1, (npages + p.pages_per_split - 1) / p.pages_per_split);
-    if (wk.split >= wk.nsplit) return;
-    wk.page_begin = wk.split * p.pages_per_split;
-    const int page_end = min(npages, wk.page_begin + p.pages_per_split);
-    wk.tile_begin = wk.page_begin * (kPage / kTileN);
-    wk.tile_end = min((wk.ctx + kTileN - 1) / kTileN, page_end * (kPage / kTileN));
-    // Cache this split's page indices in LDS (read by the wave-uniform staging code).
+    const int k = (id / 8) % p.head_groups;
+    const int r = (id / (8 * p.head_groups)) * 8 + id % 8;
+    if (r >= p.n_ranges) return;
+    const int32_t* plan = p.plan;
+    const int T = plan[2], total = plan[3];
+    const int32_t* tile_prefix = plan + kPlanHeader;
+    const int32_t* split_base = tile_prefix + p.B + 1;
+    const int32_t* num_splits = split_base + p.B + 1;
+    const int32_t* range_first_b = num_splits + p.B;
+    const int t0 = r * T, t1 = min(t0 + T, total);
+    if (t0 >= t1) return;
+    const MqaParams* params = (const MqaParams*)(__builtin_amdgcn_kernarg_segment_ptr());
     DMLA_LDS int* page_cache = reinterpret_cast<DMLA_LDS int*>(lds + kPageOffset);
-    for (int i = threadIdx.x; i < page_end - wk.page_begin; i += kThreads)
-      page_cache[i] = p.block_table[wk.b * p.bt_sb + wk.page_begin + i];
-    __syncthreads();
+    for (int bseq = range_first_b[r]; bseq < p.B; ++bseq) {
+      const int tb = tile_prefix[bseq];
+      if (tb >= t1) break;
+      const int seg0 = max(t0, tb), seg1 = min(t1, tile_prefix[bseq + 1]);
+      if (seg0 >= seg1) continue;   // an empty sequence (its output comes from the combine)
+      wk.b = bseq;
+      wk.row0 = k * kRowsPerWG;
+      wk.ctx = min(max(p.seqlens[bseq], 0), p.max_pages * kPage);
+      wk.tile_begin = seg0 - tb;
+      wk.tile_end = seg1 - tb;
+      wk.page_begin = wk.tile_begin / (kPage / kTileN);
+      wk.nsplit = num_splits[bseq];
+      wk.split = r - tb / T;
+      wk.slot = split_base[bseq] + wk.split;
+      const int page_end = (wk.tile_end + (kPage / kTileN) - 1) / (kPage / kTileN);
+      // Cache this segment's page indices in LDS (read by the wave-uniform staging code).
+      for (int i = threadIdx.x; i < page_end - wk.page_begin; i += kThreads)
+        page_cache[i] = p.block_table[bseq * p.bt_sb + wk.page_begin + i];
+      __syncthreads();
+      if (((wave >> 1) & 1) == 0) mqa_fwd_body<kDecode, 0, false>(p, params, wk, lds, wave, lane);
+      else mqa_fwd_body<kDecode, 1, false>(p, params, wk, lds, wave, lane);
+      __syncthreads();   // every LDS read of this segment is done before the next one's copies
+    }
   }
-  const MqaParams* params = (const MqaParams*)(__builtin_amdgcn_kernarg_segment_ptr());
-  if (((wave >> 1) & 1) == 0) mqa_fwd_body<kDecode, 0, false>(p, params, wk, lds, wave, lane);
-  else mqa_fwd_body<kDecode, 1, false>(p, params, wk, lds, wave, lane);
 }
 
-// Pages per split for a decode batch (at least 2, at most the table width).
-int decode_pages_per_split(int64_t B, int64_t H, int64_t max_pages) {
-  const int64_t cus = device_cu_count();
+// One workgroup computes the decode plan (layout above) from the context lengths.
+__global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlens, int B, int R, int max_pages,
+                                                           int32_t* plan) {
+  __shared__ int scan[1024];
+  int32_t* tile_prefix = plan + kPlanHeader;
+  int32_t* split_base = tile_prefix + B + 1;
+  int32_t* num_splits = split_base + B + 1;
+  int32_t* range_first_b = num_splits + B;
+  const int tid = threadIdx.x;
+  // Exclusive prefix over 1024-element chunks: Hillis-Steele within the chunk plus a carry.
+  auto chunk_scan = [&](int v) -> int {   // returns the inclusive scan; scan[1023] is the total
+    scan[tid] = v;
+    __syncthreads();
+    for (int off = 1; off < 1024; off *= 2) {
+      const int add = tid >= off ? scan[tid - off] : 0;
+      __syncthreads();
+      scan[tid] += add;
+      __syncthreads();
+    }
+    return scan[tid];
+  };
+  int carry = 0;
+  for (int base = 0; base < B; base += 1024) {
+    const int b = base + tid;
+    int nt = 0;
+    if (b < B) nt = (min(max(seqlens[b], 0), max_pages * kPage) + kTileN - 1) / kTileN;
+    const int incl = chunk_scan(nt);
+    if (b < B) tile_prefix[b] = carry + incl - nt;
+    carry += scan[1023];
+    __syncthreads();
+  }
+  const int total = carry;
+  const int T = max(1, (total + R - 1) / R);
+  if (tid == 0) tile_prefix[B] = total;
+  __threadfence_block();
+  __syncthreads();
+  int scarry = 0;
+  for (int base = 0; base < B; base += 1024) {
+    const int b = base + tid;
+    int ns = 0;
+    if (b < B) {
+      const int tb = tile_prefix[b], te = tile_prefix[b + 1];
+      ns = te > tb ? (te - 1) / T - tb / T + 1 : 0;
+      num_splits[b] = ns;
+    }
+    const int incl = chunk_scan(ns);
+    if (b < B) split_base[b] = scarry + incl - ns;
+    scarry += scan[1023];
+    __syncthreads();
+  }
+  if (tid == 0) {
+    split_base[B] = scarry;
+    plan[0] = B; plan[1] = R; plan[2] = T; plan[3] = total; plan[4] = scarry;
+    plan[5] = plan[6] = plan[7] = 0;
+  }
+  // range_first_b[r]: the last sequence b with tile_prefix[b] <= r T and a nonempty span
+  // there (binary search for the last b with tile_prefix[b] <= r T).
+  for (int r = tid; r < R; r += 1024) {
+    const int t = r * T;
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) / 2;
+      if (tile_prefix[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    range_first_b[r] = lo;
+  }
+}
+
+// Ranges of a decode plan: one workgroup per range and head group fills the CUs; more ranges
+// when the widest batch would overflow a segment's page cache.
+int64_t decode_ranges(int64_t B, int64_t H, int64_t max_pages) {
   const int64_t hg = (H + kRowsPerWG - 1) / kRowsPerWG;
-  const int64_t total = B * hg * max_pages;
-  // About one split per CU at full length: measured on cfg 3, smaller splits lose more to the
-  // per-split prologue (Q, first-tile max) and the fp32 partials than they gain in balance.
-  int64_t pps = (total + cus - 1) / cus;
-  if (pps < 2) pps = 2;
-  if (pps > max_pages) pps = max_pages;
-  if (pps > kMaxSplitPages) pps = kMaxSplitPages;
-  return (int)(pps < 1 ? 1 : pps);
+  int64_t r = device_cu_count() / hg;
+  if (r >= 8) r -= r % 8;
+  const int64_t cap = (B * max_pages * (kPage / kTileN) + kMaxSegTiles - 1) / kMaxSegTiles;
+  return std::max<int64_t>(std::max<int64_t>(r, cap), 1);
 }
 
 }  // namespace
@@ -700,22 +792,48 @@ extern "C" int dmla_fwd_cache_latent(const void* q, const void* k_lat, void* o, 
   return check_launch("dmla_fwd_cache_latent");
 }
 
-extern "C" int64_t dmla_decode_workspace_bytes(int64_t B, int64_t H, int64_t d_v, int64_t max_pages_per_seq) {
-  if (B <= 0 || H <= 0 || d_v != kDv || max_pages_per_seq <= 0) return 0;
-  const int pps = decode_pages_per_split(B, H, max_pages_per_seq);
-  const int64_t max_splits = (max_pages_per_seq + pps - 1) / pps;
-  if (max_splits <= 1) return 0;
-  return B * max_splits * H * (int64_t)(kDv + 1) * (int64_t)sizeof(float);
+// Bytes of a decode plan for this batch on the current device (a multiple of 256).
+extern "C" int64_t dmla_decode_plan_bytes(int64_t B, int64_t H, int64_t max_pages_per_seq) {
+  if (B <= 0 || H <= 0 || max_pages_per_seq <= 0) return 0;
+  const int64_t R = decode_ranges(B, H, max_pages_per_seq);
+  return (plan_ints(B, R) * 4 + 255) / 256 * 256;
 }
 
-extern "C" int dmla_decode_paged(const void* q, const void* kv_pool, const int32_t* block_table,
-                                 const int32_t* cache_seqlens, void* o, float* lse, int64_t B,
-                                 int64_t H, int64_t d_qk, int64_t d_v, int64_t page_size,
-                                 int64_t num_pages, int64_t max_pages_per_seq, int64_t q_sb,
-                                 int64_t q_sh, int64_t kv_sp, int64_t kv_ss, int64_t bt_sb,
-                                 int64_t o_sb, int64_t o_sh, float softmax_scale, void* workspace,
-                                 int64_t workspace_bytes, dmla_stream_t stream) {
+static int64_t decode_slots(int64_t B, int64_t H, int64_t max_pages_per_seq) {
+  return decode_ranges(B, H, max_pages_per_seq) + B;   // sum over sequences of their splits
+}
+
+extern "C" int64_t dmla_decode_workspace_bytes(int64_t B, int64_t H, int64_t d_v, int64_t max_pages_per_seq) {
+  if (B <= 0 || H <= 0 || d_v != kDv || max_pages_per_seq <= 0) return 0;
+  return dmla_decode_plan_bytes(B, H, max_pages_per_seq) +
+         decode_slots(B, H, max_pages_per_seq) * H * (int64_t)(kDv + 1) * (int64_t)sizeof(float);
+}
+
+extern "C" int dmla_decode_plan(const int32_t* cache_seqlens, int64_t B, int64_t H, int64_t max_pages_per_seq,
+                                int32_t* plan, int64_t plan_bytes, dmla_stream_t stream) {
   clear_error();
+  if (!cache_seqlens || !plan) return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_plan: null pointer argument");
+  if (B <= 0 || H <= 0 || max_pages_per_seq <= 0)
+    return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_plan: sizes must be positive");
+  if (H > ((int64_t)1 << 16) || B > ((int64_t)1 << 20) || max_pages_per_seq > ((int64_t)1 << 24) ||
+      B * max_pages_per_seq * (kPage / kTileN) > 0x7fffffff)
+    return fail(DMLA_ERR_UNSUPPORTED, "dmla_decode_plan: size too large");
+  const int64_t need = dmla_decode_plan_bytes(B, H, max_pages_per_seq);
+  if (plan_bytes < need)
+    return fail(DMLA_ERR_WORKSPACE, "dmla_decode_plan: %lld bytes needed (got %lld)", (long long)need,
+                (long long)plan_bytes);
+  const int64_t R = decode_ranges(B, H, max_pages_per_seq);
+  hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, cache_seqlens, (int)B, (int)R,
+                     (int)max_pages_per_seq, plan);
+  return check_launch("dmla_decode_plan");
+}
+
+// Argument checks shared by the decode entry points (before any workspace check).
+static int decode_validate(const void* q, const void* kv_pool, const int32_t* block_table,
+                           const int32_t* cache_seqlens, const void* o, int64_t B, int64_t H, int64_t d_qk,
+                           int64_t d_v, int64_t page_size, int64_t num_pages, int64_t max_pages_per_seq,
+                           int64_t q_sb, int64_t q_sh, int64_t kv_sp, int64_t kv_ss, int64_t bt_sb, int64_t o_sb,
+                           int64_t o_sh, float softmax_scale) {
   if (!q || !kv_pool || !block_table || !cache_seqlens || !o)
     return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: null pointer argument");
   if (B < 0 || H < 0 || num_pages < 0 || max_pages_per_seq < 0)
@@ -735,11 +853,32 @@ extern "C" int dmla_decode_paged(const void* q, const void* kv_pool, const int32
     return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: block_table row stride %lld < max_pages_per_seq %lld",
                 (long long)bt_sb, (long long)max_pages_per_seq);
   if (H > ((int64_t)1 << 16) || B > ((int64_t)1 << 20) || max_pages_per_seq > ((int64_t)1 << 24) ||
-      num_pages > 0x7fffffff)
+      num_pages > 0x7fffffff || B * max_pages_per_seq * (kPage / kTileN) > 0x7fffffff)
     return fail(DMLA_ERR_UNSUPPORTED, "dmla_decode_paged: size too large");
   if (B == 0 || H == 0) return DMLA_OK;
   if (num_pages == 0 || max_pages_per_seq == 0)
     return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: empty page pool or block table");
+  return DMLA_OK;
+}
+
+extern "C" int dmla_decode_paged_planned(const void* q, const void* kv_pool, const int32_t* block_table,
+                                         const int32_t* cache_seqlens, void* o, float* lse, int64_t B,
+                                         int64_t H, int64_t d_qk, int64_t d_v, int64_t page_size,
+                                         int64_t num_pages, int64_t max_pages_per_seq, int64_t q_sb,
+                                         int64_t q_sh, int64_t kv_sp, int64_t kv_ss, int64_t bt_sb,
+                                         int64_t o_sb, int64_t o_sh, float softmax_scale, const int32_t* plan,
+                                         void* workspace, int64_t workspace_bytes, dmla_stream_t stream) {
+  clear_error();
+  if (!plan) return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: null plan");
+  int rc0 = decode_validate(q, kv_pool, block_table, cache_seqlens, o, B, H, d_qk, d_v, page_size, num_pages,
+                            max_pages_per_seq, q_sb, q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale);
+  if (rc0 != DMLA_OK || B == 0 || H == 0) return rc0;
+  const int64_t slots = decode_slots(B, H, max_pages_per_seq);
+  const int64_t need = slots * H * (int64_t)(kDv + 1) * (int64_t)sizeof(float);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(DMLA_ERR_WORKSPACE, "dmla_decode_paged: workspace of %lld bytes needed (got %lld)",
+                (long long)need, (long long)workspace_bytes);
+  if (!aligned16(workspace)) return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: workspace must be 16-byte aligned");
 
   MqaParams p = {};
   p.q = static_cast<const bf16*>(q);
@@ -756,35 +895,55 @@ extern "C" int dmla_decode_paged(const void* q, const void* kv_pool, const int32
   p.bt_sb = bt_sb;
   p.num_pages = (int)num_pages;
   p.max_pages = (int)max_pages_per_seq;
-  p.pages_per_split = decode_pages_per_split(B, H, max_pages_per_seq);
-  p.max_splits = (int)((max_pages_per_seq + p.pages_per_split - 1) / p.pages_per_split);
   p.head_groups = (int)((H + kRowsPerWG - 1) / kRowsPerWG);
-  p.n_units = (int)(B * p.max_splits);
-  if (p.max_splits > 1) {
-    const int64_t need = dmla_decode_workspace_bytes(B, H, d_v, max_pages_per_seq);
-    if (workspace == nullptr || workspace_bytes < need)
-      return fail(DMLA_ERR_WORKSPACE, "dmla_decode_paged: workspace of %lld bytes needed (got %lld)",
-                  (long long)need, (long long)workspace_bytes);
-    if (!aligned16(workspace)) return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: workspace must be 16-byte aligned");
-    p.part_o = static_cast<float*>(workspace);
-    p.part_lse = p.part_o + B * p.max_splits * H * kDv;
-  }
-  const int64_t grid = (((int64_t)p.n_units + 7) / 8) * 8 * p.head_groups;
+  p.n_ranges = (int)decode_ranges(B, H, max_pages_per_seq);
+  p.plan = plan;
+  p.part_o = static_cast<float*>(workspace);
+  p.part_lse = p.part_o + slots * H * kDv;
+  const int64_t grid = ((int64_t)(p.n_ranges + 7) / 8) * 8 * p.head_groups;
   if (grid > 0x7fffffff) return fail(DMLA_ERR_UNSUPPORTED, "dmla_decode_paged: grid too large");
   hipLaunchKernelGGL(mqa_fwd_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream, p);
   int rc = check_launch("dmla_decode_paged");
-  if (rc != DMLA_OK || p.max_splits == 1) return rc;
+  if (rc != DMLA_OK) return rc;
+  // Sequences with one split were written by the decode kernel; the others (and the empty
+  // ones: zeros, lse -inf) come from the combine.
+  const int32_t* tile_prefix = plan + kPlanHeader;
   CombineArgs c = {};
   c.part_o = p.part_o;
   c.part_lse = p.part_lse;
-  c.seqlens = cache_seqlens;
+  c.split_base = tile_prefix + B + 1;
+  c.num_splits = tile_prefix + 2 * (B + 1);
   c.o = p.o;
   c.lse = lse;
-  c.B = (int)B; c.H = (int)H; c.max_splits = p.max_splits; c.d = kDv;
-  c.pages_per_split = p.pages_per_split; c.page_size = kPage; c.max_pages = p.max_pages;
+  c.B = (int)B; c.H = (int)H; c.max_splits = p.n_ranges + 1; c.d = kDv;
   c.skip_single = 1;
-  c.po_sb = (int64_t)p.max_splits * H * kDv; c.po_ss = H * kDv; c.po_sh = kDv;
-  c.lse_sb = (int64_t)p.max_splits * H; c.lse_ss = H; c.lse_sh = 1;
+  c.po_ss = H * kDv; c.po_sh = kDv;
+  c.lse_ss = H; c.lse_sh = 1;
   c.o_sb = o_sb; c.o_sh = o_sh;
   return launch_lse_combine(c, (hipStream_t)stream, "dmla_decode_paged(combine)");
+}
+
+extern "C" int dmla_decode_paged(const void* q, const void* kv_pool, const int32_t* block_table,
+                                 const int32_t* cache_seqlens, void* o, float* lse, int64_t B,
+                                 int64_t H, int64_t d_qk, int64_t d_v, int64_t page_size,
+                                 int64_t num_pages, int64_t max_pages_per_seq, int64_t q_sb,
+                                 int64_t q_sh, int64_t kv_sp, int64_t kv_ss, int64_t bt_sb,
+                                 int64_t o_sb, int64_t o_sh, float softmax_scale, void* workspace,
+                                 int64_t workspace_bytes, dmla_stream_t stream) {
+  clear_error();
+  int rc0 = decode_validate(q, kv_pool, block_table, cache_seqlens, o, B, H, d_qk, d_v, page_size, num_pages,
+                            max_pages_per_seq, q_sb, q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale);
+  if (rc0 != DMLA_OK || B == 0 || H == 0) return rc0;
+  const int64_t need = dmla_decode_workspace_bytes(B, H, d_v, max_pages_per_seq);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(DMLA_ERR_WORKSPACE, "dmla_decode_paged: workspace of %lld bytes needed (got %lld)",
+                (long long)need, (long long)workspace_bytes);
+  if (!aligned16(workspace)) return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: workspace must be 16-byte aligned");
+  const int64_t pb = dmla_decode_plan_bytes(B, H, max_pages_per_seq);
+  int rc = dmla_decode_plan(cache_seqlens, B, H, max_pages_per_seq, static_cast<int32_t*>(workspace), pb, stream);
+  if (rc != DMLA_OK) return rc;
+  return dmla_decode_paged_planned(q, kv_pool, block_table, cache_seqlens, o, lse, B, H, d_qk, d_v, page_size,
+                                   num_pages, max_pages_per_seq, q_sb, q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh,
+                                   softmax_scale, static_cast<const int32_t*>(workspace),
+                                   static_cast<char*>(workspace) + pb, workspace_bytes - pb, stream);
 }

@@ -24,13 +24,16 @@ int device_cu_count();
 
 // Split-KV combine (dmla_cache.hip): part_o [.., split, .., d] fp32 partial outputs, each
 // normalised over its split, and part_lse natural-log sums, addressed by element strides.
-// The split count of sequence b is num_splits[b] when given, else derived from seqlens[b] and
-// pages_per_split when given, else max_splits.  skip_single leaves sequences with one split
-// untouched (their rows were written by the producer directly).
+// The split count of sequence b is num_splits[b] (at most max_splits) when given, else
+// derived from seqlens[b] and pages_per_split when given, else max_splits.  Split s of
+// sequence b is at b * sb + s * ss, or at (split_base[b] + s) * ss when split_base is given.
+// skip_single leaves sequences with one split untouched (their rows were written by the
+// producer directly).
 struct CombineArgs {
   const float* part_o;
   const float* part_lse;
   const int32_t* num_splits;
+  const int32_t* split_base;
   const int32_t* seqlens;
   __bf16* o;
   float* lse;                 // nullable, [B, H] contiguous

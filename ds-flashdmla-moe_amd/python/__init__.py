@@ -8,6 +8,7 @@ from .ops import (  # noqa: F401
     flash_dmla,
     flash_dmla_bwd,
     flash_dmla_decode_paged,
+    flash_dmla_decode_plan,
     flash_dmla_fwd,
     flash_dmla_fwd_onthefly,
     flash_dmla_kv_append,

@@ -133,6 +133,23 @@ def flash_dmla_fwd_onthefly(
     return (o, m, l) if return_stats else o
 
 
+def flash_dmla_decode_plan(cache_seqlens: torch.Tensor, num_heads: int, max_pages: int) -> torch.Tensor:
+    """Decode tile-scheduler plan (int32 tensor) for this batch on the current device.
+
+    It depends on cache_seqlens only, so one plan serves every layer of a decode step: pass it
+    to flash_dmla_decode_paged(..., plan=plan).  Layout in include/flashdmla.h.
+    """
+    _require(cache_seqlens.dtype == torch.int32 and cache_seqlens.dim() == 1 and cache_seqlens.is_cuda
+             and cache_seqlens.is_contiguous(), "cache_seqlens must be a contiguous 1-D int32 GPU tensor")
+    B = cache_seqlens.shape[0]
+    nbytes = int(_lib.lib().dmla_decode_plan_bytes(B, num_heads, max_pages))
+    _require(nbytes > 0, "decode plan: B, num_heads and max_pages must be positive")
+    plan = torch.empty((nbytes // 4,), dtype=torch.int32, device=cache_seqlens.device)
+    _lib.call("dmla_decode_plan", _ptr(cache_seqlens), B, num_heads, max_pages, _ptr(plan), nbytes,
+              _stream(cache_seqlens))
+    return plan
+
+
 def flash_dmla_decode_paged(
     q: torch.Tensor,
     kv_pool: torch.Tensor,
@@ -142,6 +159,7 @@ def flash_dmla_decode_paged(
     softmax_scale: Optional[float] = None,
     return_lse: bool = False,
     check_indices: bool = False,
+    plan: Optional[torch.Tensor] = None,
 ):
     """Paged-KV DMLA decode for one query token per sequence.
 
@@ -149,7 +167,8 @@ def flash_dmla_decode_paged(
     cache_seqlens [B] int32.  Returns o [B, H, d_v] bf16 (and lse [B, H] fp32 natural log when
     return_lse).  Token t of sequence b is kv_pool[block_table[b, t // 64], t % 64].
     check_indices=True validates the table and lengths on the host (one device sync) and raises
-    instead of producing NaN rows for out-of-range pages.
+    instead of producing NaN rows for out-of-range pages.  plan: a flash_dmla_decode_plan of
+    the same cache_seqlens, H and max_pages (computed here when None).
     """
     _check_bf16("q", q, 3)
     _check_bf16("kv_pool", kv_pool, 3)
@@ -179,15 +198,30 @@ def flash_dmla_decode_paged(
     o = torch.empty((B, H, d_v), dtype=torch.bfloat16, device=q.device)
     lse = torch.empty((B, H), dtype=torch.float32, device=q.device) if return_lse else None
     ws_bytes = int(_lib.lib().dmla_decode_workspace_bytes(B, H, d_v, max_pages))
-    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
-    _lib.call(
-        "dmla_decode_paged",
-        _ptr(q), _ptr(kv_pool), _ptr(block_table), _ptr(cache_seqlens), _ptr(o), _ptr(lse),
-        B, H, Dqk, d_v, page, num_pages, max_pages,
-        q.stride(0), q.stride(1), kv_pool.stride(0), kv_pool.stride(1), block_table.stride(0),
-        o.stride(0), o.stride(1),
-        _scale(softmax_scale, Dqk), _ptr(ws), ws_bytes, _stream(q),
-    )
+    if plan is None:
+        ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
+        _lib.call(
+            "dmla_decode_paged",
+            _ptr(q), _ptr(kv_pool), _ptr(block_table), _ptr(cache_seqlens), _ptr(o), _ptr(lse),
+            B, H, Dqk, d_v, page, num_pages, max_pages,
+            q.stride(0), q.stride(1), kv_pool.stride(0), kv_pool.stride(1), block_table.stride(0),
+            o.stride(0), o.stride(1),
+            _scale(softmax_scale, Dqk), _ptr(ws), ws_bytes, _stream(q),
+        )
+    else:
+        plan_bytes = int(_lib.lib().dmla_decode_plan_bytes(B, H, max_pages))
+        _require(plan.dtype == torch.int32 and plan.is_cuda and plan.is_contiguous()
+                 and plan.numel() * 4 >= plan_bytes, "plan must come from flash_dmla_decode_plan for this batch")
+        ws_bytes -= plan_bytes
+        ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
+        _lib.call(
+            "dmla_decode_paged_planned",
+            _ptr(q), _ptr(kv_pool), _ptr(block_table), _ptr(cache_seqlens), _ptr(o), _ptr(lse),
+            B, H, Dqk, d_v, page, num_pages, max_pages,
+            q.stride(0), q.stride(1), kv_pool.stride(0), kv_pool.stride(1), block_table.stride(0),
+            o.stride(0), o.stride(1),
+            _scale(softmax_scale, Dqk), _ptr(plan), _ptr(ws), ws_bytes, _stream(q),
+        )
     return (o, lse) if return_lse else o
 
 

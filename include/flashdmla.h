@@ -108,6 +108,9 @@ int dmla_fwd_onthefly(const void* q, const void* k, const void* v, const void* w
  * max_pages_per_seq * page_size are clamped to it.  A page index outside [0, num_pages) is
  * never dereferenced: the sequence's output and lse are set to NaN instead.
  * Supported: d_qk = 576, d_v = 512, page_size = 64.
+ *
+ * dmla_decode_paged computes a decode plan (dmla_decode_plan) at the head of the workspace,
+ * then runs dmla_decode_paged_planned on the rest.  The workspace is always required.
  */
 int64_t dmla_decode_workspace_bytes(int64_t B, int64_t H, int64_t d_v, int64_t max_pages_per_seq);
 int dmla_decode_paged(const void* q, const void* kv_pool, const int32_t* block_table,
@@ -117,6 +120,35 @@ int dmla_decode_paged(const void* q, const void* kv_pool, const int32_t* block_t
                       int64_t kv_ss, int64_t bt_sb, int64_t o_sb, int64_t o_sh,
                       float softmax_scale, void* workspace, int64_t workspace_bytes,
                       dmla_stream_t stream);
+
+/*
+ * Decode tile-scheduler plan, computed on the device from cache_seqlens (no reference
+ * counterpart; the step between the block table and the decode kernel).  The 32-token key
+ * tiles of all sequences, in order, are cut into R equal ranges (R = CUs / head groups of 64
+ * heads, more if one range's pages would exceed 1024), each processed by one workgroup per
+ * head group, so the work per workgroup does not depend on how the lengths are distributed.
+ * A range that spans sequences contributes one split to each; sequences with several splits
+ * are merged by the LSE combine.  plan (int32, dmla_decode_plan_bytes bytes):
+ *   [0..7]   B, R, T (tiles per range), total tiles, total splits, 0, 0, 0
+ *   then     tile_prefix[B + 1], split_base[B + 1], num_splits[B], range_first_b[R]
+ * A plan depends on cache_seqlens only, so one plan serves every layer of a decode step.
+ */
+int64_t dmla_decode_plan_bytes(int64_t B, int64_t H, int64_t max_pages_per_seq);
+int dmla_decode_plan(const int32_t* cache_seqlens, int64_t B, int64_t H, int64_t max_pages_per_seq,
+                     int32_t* plan, int64_t plan_bytes, dmla_stream_t stream);
+
+/*
+ * dmla_decode_paged with a precomputed plan for the same B, H, max_pages_per_seq and
+ * cache_seqlens on this device.  workspace holds the split partials:
+ * dmla_decode_workspace_bytes - dmla_decode_plan_bytes bytes.
+ */
+int dmla_decode_paged_planned(const void* q, const void* kv_pool, const int32_t* block_table,
+                              const int32_t* cache_seqlens, void* o, float* lse, int64_t B, int64_t H,
+                              int64_t d_qk, int64_t d_v, int64_t page_size, int64_t num_pages,
+                              int64_t max_pages_per_seq, int64_t q_sb, int64_t q_sh, int64_t kv_sp,
+                              int64_t kv_ss, int64_t bt_sb, int64_t o_sb, int64_t o_sh,
+                              float softmax_scale, const int32_t* plan, void* workspace,
+                              int64_t workspace_bytes, dmla_stream_t stream);
 
 /*
  * Paged latent-cache append: writes new rows into the pages the decode reads.
@@ -153,7 +185,8 @@ int dmla_kv_append(void* kv_pool, const int32_t* block_table, const int32_t* cac
  *   lse      [B, H]       fp32 contiguous; may be NULL
  *
  *   o = sum_s w_s o_s / sum_s w_s with w_s = exp(lse_s - max_s lse_s), lse = max + log(sum w);
- *   a sequence whose splits all have lse = -inf gets o = 0 and lse = -inf.  d % 4 == 0.
+ *   a sequence whose splits all have lse = -inf gets o = 0 and lse = -inf; a NaN lse in any
+ *   split makes o and lse NaN.  d % 4 == 0.
  */
 int dmla_lse_combine(const float* part_o, const float* part_lse, const int32_t* num_splits, void* o,
                      float* lse, int64_t B, int64_t H, int64_t max_splits, int64_t d, int64_t po_sb,

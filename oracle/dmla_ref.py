@@ -72,6 +72,10 @@ def attention_exact(q: Tensor, k: Tensor, v: Tensor, scale: float, causal: bool
     the l > 0 guard of fa_fwd.cu:117-118 (fully masked rows give o = 0, m = -inf, l = 0).
     """
     s = masked_scores(q, k, scale, causal)
+    if s.shape[-1] == 0:   # no keys at all: every row is fully masked
+        m = torch.full(s.shape[:-1], float("-inf"), dtype=s.dtype, device=s.device)
+        return (torch.zeros(s.shape[:-1] + (v.shape[-1],), dtype=s.dtype, device=s.device), m,
+                torch.zeros_like(m))
     m = s.amax(dim=-1)
     m_safe = torch.where(torch.isfinite(m), m, torch.zeros_like(m))
     e = torch.exp(s - m_safe.unsqueeze(-1))
@@ -179,6 +183,27 @@ def dmla_decode_paged(q: Tensor, kv_pool: Tensor, block_table: Tensor, cache_seq
     return torch.stack(outs), torch.stack(lses)
 
 
+def decode_plan(cache_seqlens, n_ranges: int, max_pages: int, page_size: int = 64, tile: int = 32):
+    """The decode tile-scheduler plan for R = n_ranges (no reference counterpart): 32-token
+    tiles of all sequences in order, cut into R ranges of T = ceil(total / R) tiles (T >= 1).
+    Returns the int32 list header[8] + tile_prefix[B+1] + split_base[B+1] + num_splits[B] +
+    range_first_b[R] with the layout of include/flashdmla.h."""
+    B = len(cache_seqlens)
+    tiles = [(min(max(int(x), 0), max_pages * page_size) + tile - 1) // tile for x in cache_seqlens]
+    tp = [0]
+    for n in tiles:
+        tp.append(tp[-1] + n)
+    total = tp[-1]
+    T = max(1, -(-total // n_ranges))
+    ns = [(tp[b + 1] - 1) // T - tp[b] // T + 1 if tp[b + 1] > tp[b] else 0 for b in range(B)]
+    sb = [0]
+    for n in ns:
+        sb.append(sb[-1] + n)
+    # the sequence holding tile r*T: the last b with tile_prefix[b] <= r*T
+    rfb = [max(b for b in range(B) if tp[b] <= r * T) for r in range(n_ranges)]
+    return [B, n_ranges, T, total, sb[-1], 0, 0, 0] + tp + sb + ns + rfb
+
+
 def kv_append(kv_pool: Tensor, block_table: Tensor, cache_seqlens: Tensor, new_kv: Tensor,
               new_lens: Optional[Tensor] = None) -> Tensor:
     """Paged KV-cache append (no reference counterpart; the producer side of gather_pages).
@@ -201,7 +226,8 @@ def lse_combine(part_o: Tensor, part_lse: Tensor, num_splits: Optional[Tensor] =
     """Merges split-KV partials: part_o [B, S, H, D] (each normalised over its split's keys),
     part_lse [B, S, H] natural log.  o = sum_s w_s o_s / sum_s w_s with w_s = exp(lse_s - max),
     lse = max + log(sum_s w_s); splits >= num_splits[b] are ignored; no finite lse -> o = 0,
-    lse = -inf.  The combine of split-KV decoding (no reference counterpart)."""
+    lse = -inf; a NaN lse -> o and lse NaN.  The combine of split-KV decoding (no reference
+    counterpart)."""
     B, S = part_o.shape[0], part_o.shape[1]
     po, pl = part_o.to(dtype), part_lse.to(dtype)
     if num_splits is not None:
@@ -211,8 +237,14 @@ def lse_combine(part_o: Tensor, part_lse: Tensor, num_splits: Optional[Tensor] =
     ref = torch.where(torch.isfinite(mx), mx, torch.zeros_like(mx))
     w = torch.exp(pl - ref.unsqueeze(1))
     wsum = w.sum(dim=1)
-    o = (w.unsqueeze(-1) * torch.nan_to_num(po)).sum(dim=1) / torch.where(wsum > 0, wsum, torch.ones_like(wsum)).unsqueeze(-1)
-    lse = torch.where(wsum > 0, ref + torch.log(torch.where(wsum > 0, wsum, torch.ones_like(wsum))), mx)
+    # an empty split (lse -inf) contributes nothing whatever its o holds; NaN propagates
+    contrib = torch.where(torch.isneginf(pl).unsqueeze(-1), torch.zeros_like(po), w.unsqueeze(-1) * po)
+    den = torch.where(wsum > 0, wsum, torch.ones_like(wsum))
+    o = contrib.sum(dim=1) / den.unsqueeze(-1)
+    lse = torch.where(wsum > 0, ref + torch.log(den), mx)
+    bad = torch.isnan(pl).any(dim=1)
+    o = torch.where(bad.unsqueeze(-1), torch.full_like(o, float("nan")), o)
+    lse = torch.where(bad, torch.full_like(lse, float("nan")), lse)
     return o, lse
 
 

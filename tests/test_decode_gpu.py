@@ -97,3 +97,56 @@ def test_decode_config3_full_shape(gpu):
     lens = torch.randint(1024, 8193, (64,), generator=g).tolist()
     q, pool, table, sl = _paged(lens, 128, seed=3, poison_tail=False)
     _check(gpu, q, pool, table, sl, oracle_device="gpu")
+
+
+def _lse_close(lse, lse_ref, tol=1e-3):
+    lse, lse_ref = lse.cpu(), lse_ref.cpu()
+    inf = torch.isinf(lse_ref)
+    assert torch.equal(torch.isinf(lse), inf) and bool((lse[inf] == lse_ref[inf]).all())
+    if (~inf).any():
+        d = (lse[~inf] - lse_ref[~inf]).abs().max().item()
+        assert d <= tol, f"lse max-abs {d:.3e}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lens,max_pages", [
+    ([5, 0, 70, 1, 64, 0, 4000, 31], 64),
+    ([8192] * 3 + [1] * 40, 128),
+    ([0, 0, 0], 4),
+    (list(range(1, 3000, 37)), 48),
+])
+def test_decode_plan_matches_oracle(gpu, lens, max_pages):
+    sl = torch.tensor(lens, dtype=torch.int32)
+    plan = ops.flash_dmla_decode_plan(sl.to(gpu), 128, max_pages).cpu().tolist()
+    nr = plan[1]
+    ref = R.decode_plan(lens, nr, max_pages)
+    assert plan[:len(ref)] == ref
+
+
+@pytest.mark.gpu
+def test_decode_ranges_spanning_many_sequences_and_empty_ones(gpu):
+    # 300 short sequences (some empty): each range covers many of them, most sequences are split
+    g = torch.Generator().manual_seed(77)
+    lens = torch.randint(0, 160, (300,), generator=g).tolist()
+    lens[:5] = [0, 0, 1, 0, 159]
+    q, pool, table, sl = _paged(lens, 128, seed=78)
+    o, lse = ops.flash_dmla_decode_paged(q.to(gpu), pool.to(gpu), table.to(gpu), sl.to(gpu), 512, SCALE,
+                                         return_lse=True)
+    o_ref, lse_ref = R.dmla_decode_paged(q.float(), pool.float(), table, sl, 512, SCALE)
+    assert_out_close(o, o_ref)
+    _lse_close(lse, lse_ref)
+    empty = sl == 0
+    assert bool((o.cpu()[empty] == 0).all())
+
+
+@pytest.mark.gpu
+def test_decode_with_a_shared_plan_is_bit_identical(gpu):
+    lens = [3000, 17, 0, 8000, 640]
+    q, pool, table, sl = _paged(lens, 128, seed=91)
+    q2 = seeded(tuple(q.shape), 92, 0.5, torch.bfloat16)
+    args = (pool.to(gpu), table.to(gpu), sl.to(gpu), 512, SCALE)
+    plan = ops.flash_dmla_decode_plan(sl.to(gpu), 128, table.shape[1])
+    for qq in (q, q2):   # one plan, two "layers"
+        a, la = ops.flash_dmla_decode_paged(qq.to(gpu), *args, return_lse=True)
+        b, lb = ops.flash_dmla_decode_paged(qq.to(gpu), *args, return_lse=True, plan=plan)
+        assert torch.equal(a, b) and torch.equal(la, lb)

@@ -281,3 +281,47 @@ def test_lse_combine_of_key_splits_is_full_attention():
     # no finite lse -> o = 0, lse = -inf
     o3, l3 = R.lse_combine(po[:, 1:2], pl[:, 1:2], dtype=torch.float64)
     assert torch.all(o3 == 0) and torch.all(torch.isneginf(l3))
+
+
+# ---------------------------------------------------------------- decode plan
+@pytest.mark.parametrize("lens,nr", [([5, 0, 70, 1, 64, 0], 4), ([1000, 3000, 10, 8192], 16), ([0, 0], 3), ([33], 8)])
+def test_decode_plan_covers_every_tile_once(lens, nr):
+    max_pages = 128
+    plan = R.decode_plan(lens, nr, max_pages)
+    B = len(lens)
+    hdr, tp = plan[:8], plan[8:8 + B + 1]
+    sb = plan[8 + B + 1:8 + 2 * (B + 1)]
+    ns = plan[8 + 2 * (B + 1):8 + 2 * (B + 1) + B]
+    rfb = plan[8 + 2 * (B + 1) + B:]
+    assert hdr[0] == B and hdr[1] == nr and len(rfb) == nr
+    T, total = hdr[2], hdr[3]
+    assert total == sum((x + 31) // 32 for x in lens) and T == max(1, -(-total // nr))
+    # walk the ranges like the decode kernel: every (sequence, tile) exactly once, splits counted
+    seen, splits = {}, [0] * B
+    for r in range(nr):
+        t0, t1 = r * T, min(r * T + T, total)
+        if t0 >= t1:
+            continue
+        b = rfb[r]
+        assert tp[b] <= t0 < tp[b + 1]
+        while b < B and tp[b] < t1:
+            s0, s1 = max(t0, tp[b]), min(t1, tp[b + 1])
+            if s0 < s1:
+                assert r - tp[b] // T == splits[b]          # split index = order of the pieces
+                splits[b] += 1
+                for t in range(s0, s1):
+                    assert (b, t - tp[b]) not in seen
+                    seen[(b, t - tp[b])] = r
+            b += 1
+    assert len(seen) == total
+    assert splits == ns and sb == [sum(ns[:i]) for i in range(B + 1)] and hdr[4] == sum(ns)
+
+
+def test_attention_with_no_keys_is_the_fully_masked_case():
+    q = torch.randn(2, 3, 8, dtype=torch.float64)
+    k = torch.zeros(2, 0, 8, dtype=torch.float64)
+    o, m, l = R.attention_exact(q, k, k[..., :4], 0.5, False)
+    assert o.shape == (2, 3, 4) and torch.all(o == 0) and torch.all(torch.isneginf(m)) and torch.all(l == 0)
+    o2, lse = R.dmla_decode_paged(torch.randn(2, 4, 16), torch.randn(3, 64, 16), torch.zeros(2, 1, dtype=torch.int32),
+                                  torch.tensor([0, 5]), 8, 0.3)
+    assert torch.all(o2[0] == 0) and torch.all(torch.isneginf(lse[0])) and torch.isfinite(lse[1]).all()
