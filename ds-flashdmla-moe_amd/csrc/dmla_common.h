@@ -95,6 +95,12 @@ __device__ __forceinline__ void dma16_after(const void* sbase, unsigned voff, un
                : "s"(sl), "v"(voff), "s"(reinterpret_cast<const void*>(sb)), "v"(d0), "v"(d1), "v"(d2), "v"(d3)
                : "m0");
 }
+// A 4-byte global -> LDS load per lane (lane l writes lds_addr + 4 l): used to pull lines into
+// L2 ahead of their real copies; the LDS bytes written are a scratch area nobody reads.
+__device__ __forceinline__ void dma4_addr(const void* gaddr, unsigned lds_addr) {
+  const unsigned sl = __builtin_amdgcn_readfirstlane(lds_addr);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" : : "s"(sl), "v"(gaddr) : "memory", "m0");
+}
 // Same copy with a full 64-bit global address per lane (rows of one tile that are far apart,
 // e.g. query rows of different heads).
 __device__ __forceinline__ void dma16_addr(const void* gaddr, unsigned lds_addr) {
@@ -194,5 +200,7 @@ __device__ __forceinline__ float group_sum(float v) {
 
 // Wait until every outstanding vector-memory op of this wave (including LDS DMA) has landed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); /* gfx9 encoding: vmcnt(0) expcnt(7) lgkmcnt(15) */ }
+// All but the most recent vector-memory load done (loads retire in issue order).
+__device__ __forceinline__ void wait_vmem_but_one() { __builtin_amdgcn_s_waitcnt(0x0f71); /* vmcnt(1) */ }
 
 }  // namespace dmla

@@ -49,7 +49,7 @@ constexpr int kKcHalf = kDqk / 32 / 2;              // 9 k-steps per dims half
 constexpr int kDbWave = kDv / 16 / kWaves;          // 4 output column blocks (64 columns) per wave
 constexpr int kXBytes = kWaves * 1024;              // partial-score exchange, one buffer
 constexpr int kPBytes = 4 * 1024;                   // P of the 64 rows as MFMA B operands
-constexpr int kMaxSplitPages = 1024;                // page-table cache of one decode split
+constexpr int kMaxSegPages = 128;                   // page indices of a decode segment: two VGPRs
 constexpr int kXOffset = kRing * kTileBytes;
 constexpr int kPOffset = kXOffset + 2 * kXBytes;
 constexpr int kRowOffset = kPOffset + 2 * kPBytes;  // per-row exchange [3][2 key halves][64]
@@ -63,7 +63,8 @@ constexpr int kQRowBytes = kDqk * 2 + 16;
 constexpr int kQChunks = kRowsPerWG * kQRowBytes / 16;   // 4672 16-byte chunks, 73 per row
 constexpr int kQOffset = kTileBytes;
 static_assert(kQOffset + kRowsPerWG * kQRowBytes <= kXOffset + kXBytes, "Q staging fits before buffer 1");
-constexpr int kLdsBytes = kPageOffset + kMaxSplitPages * 4;
+constexpr int kTouchOffset = kPageOffset;   // 256 B written by decode's L2 pulls
+constexpr int kLdsBytes = kTouchOffset + 256;
 constexpr float kHeadroom = 32.0f;                  // log2 headroom of p over the reference max
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 static_assert(kPage % kTileN == 0, "a page holds whole tiles");
@@ -125,7 +126,7 @@ struct Work {
 // tile_prefix[B + 1], split_base[B + 1] (first partial slot of each sequence), num_splits[B],
 // range_first_b[R] (the sequence containing the range's first tile).
 constexpr int kPlanHeader = 8;
-constexpr int kMaxSegTiles = 2 * kMaxSplitPages - 2;   // a segment's pages fit the page cache
+constexpr int kMaxSegTiles = 2 * kMaxSegPages - 2;   // a segment's pages fit its page registers
 __host__ __device__ inline int64_t plan_ints(int64_t B, int64_t R) { return kPlanHeader + 3 * B + 2 + R; }
 
 template <bool kDecode, int kHalf>
@@ -148,7 +149,6 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   DMLA_LDS char* pbuf = lds + kPOffset;
   DMLA_LDS float* rowx = reinterpret_cast<DMLA_LDS float*>(lds + kRowOffset);
   DMLA_LDS int* flags = reinterpret_cast<DMLA_LDS int*>(lds + kFlagOffset);
-  const DMLA_LDS int* page_cache = reinterpret_cast<const DMLA_LDS int*>(lds + kPageOffset);
 
   const int nrows = kDecode ? p.H : p.H * p.Sq;
   const int own_row = row0 + 16 * rb + l16;
@@ -175,6 +175,13 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   // chunk (l%8) ^ swz(row); the group's 128-byte column offset goes into the scalar base (an
   // instruction offset would also move the LDS address).
   bool bad_page = false;
+  int seg_pages[2] = {0, 0};
+  if constexpr (kDecode) {
+    const int npg = (tile_end + (kPage / kTileN) - 1) / (kPage / kTileN) - wk.page_begin;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (64 * h + lane < npg) seg_pages[h] = p.block_table[b * p.bt_sb + wk.page_begin + 64 * h + lane];
+  }
   const int row_stride_bytes = (int)(p.k_ss * 2);
   // Row 8r + l/8 of a copy has swizzle swz(8 (r & 1) + l/8): two column variants per lane.
   const int dma_lrow = lane >> 3;
@@ -194,9 +201,16 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
       valid_rows = p.Sk - tile * kTileN;
       return reinterpret_cast<const char*>(p.kv + b * p.k_sb + (int64_t)tile * kTileN * p.k_ss);
     } else {
-      const int pg = tile / (kPage / kTileN);
-      int page = uniform(page_cache[pg - wk.page_begin]);
-      if (page < 0 || page >= p.num_pages) { bad_page = true; page = 0; }
+      // The segment's page indices sit in two VGPRs, lane i holding pages i and 64 + i of it:
+      // a lane read gives the index in an SGPR, with no memory access or wait.
+      // Branch-free (selects on scalars), so the pipelined iteration stays one basic block.
+      const int idx = tile / (kPage / kTileN) - wk.page_begin;
+      const int pa = __builtin_amdgcn_readlane(seg_pages[0], idx & 63);
+      const int pb = __builtin_amdgcn_readlane(seg_pages[1], idx & 63);
+      int page = idx < 64 ? pa : pb;
+      const bool bad = page < 0 || page >= p.num_pages;
+      bad_page = bad_page || bad;
+      page = bad ? 0 : page;
       valid_rows = wk.ctx - tile * kTileN;
       return reinterpret_cast<const char*>(p.kv + (int64_t)page * p.k_sb +
                                            (int64_t)(tile % (kPage / kTileN)) * kTileN * p.k_ss);
@@ -320,6 +334,24 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   using CopyOn = std::integral_constant<int, 1>;
   using CopyOff = std::integral_constant<int, 0>;
   using CopyAfterPv = std::integral_constant<int, 2>;
+  // Decode reads its tiles from HBM, with the copies of tile t+2 due one iteration later: each
+  // iteration also pulls the 288 lines of tile t+4 into L2 with one 4-byte load per lane
+  // (lane l of wave w: line (64 w + l) mod 288), so the real copy two iterations on hits L2.
+  // Every step that issues copies ends with exactly one such load, and the waits for a tile's
+  // copies leave the newest load outstanding (wait_tile); the prefill's tiles are L2-resident.
+  constexpr bool kPull = kDecode && !kExact;
+  auto pull = [&](int tile) {
+    if constexpr (kPull) {
+      int unused_rows;
+      const char* src = tile_src(tile, unused_rows);
+      const int i = (64 * wave + lane) % (kTileN * kGroups);
+      dma4_addr(src + (i / kGroups) * row_stride_bytes + (i % kGroups) * 128, lds_base + kTouchOffset);
+    }
+  };
+  auto wait_tile = [&]() {
+    if constexpr (kPull) wait_vmem_but_one();
+    else wait_vmem();
+  };
   auto post_partial = [&](int tq, const f32x4 (&sacc)[2]) {
     *reinterpret_cast<DMLA_LDS f32x4*>(xbuf + (tq & 1) * kXBytes + x_post) = sacc[1 - kHalf];
   };
@@ -351,6 +383,9 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   // ---- Q through LDS, with the first key tile in flight beside it ---------------------------
   // Chunk k of the staging area is 16-byte chunk k % 73 of row k / 73 (chunk 72 is the row's
   // padding and re-reads chunk 0); rows past the last one re-read row 0 of the item.
+  // (The first tile's copies go out before Q's: for decode, tile_src waits for the page-index
+  // loads, which would otherwise also drain the Q copies issued after them.)
+  if (tile_begin < tile_end) stage(tile_begin, tile_begin);
   {
     const unsigned qbase = lds_base + kQOffset;
     for (int i = wave; i * 64 < kQChunks; i += kWaves) {
@@ -368,7 +403,6 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
       dma16_addr(qrow + 8 * (ch < kDqk / 8 ? ch : 0), qbase + i * 1024);
     }
   }
-  if (tile_begin < tile_end) stage(tile_begin, tile_begin);
   wait_vmem();
   __syncthreads();
 #pragma unroll
@@ -415,6 +449,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     }
     if (tile_begin + 1 < tile_end) qk(tile_begin, sacc, tile_begin + 1, CopyOn{});
     else qk(tile_begin, sacc, tile_begin + 1, CopyOff{});
+    pull(tile_begin + 3);
     post_partial(tile_begin, sacc);
     if constexpr (!kExact) {
       __syncthreads();
@@ -436,11 +471,14 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     // trigger it are rare, and a per-tile exchange of flags would cost every tile LDS traffic.
     auto iteration = [&](int t, auto kind_tag) {
       constexpr int kKind = decltype(kind_tag)::value;
-      wait_vmem();       // this wave's copies of tile t+1 have landed
+      wait_tile();       // this wave's copies of tile t+1 have landed
       __syncthreads();   // partials(t) and P(t-1) posted; tile t+1 complete
       const f32x4 s = take_scores(t, sacc);
       pv(t - 1);
-      if constexpr (kKind == 0) qk(t + 1, sacc, t + 2, CopyAfterPv{});
+      if constexpr (kKind == 0) {
+        qk(t + 1, sacc, t + 2, CopyAfterPv{});
+        pull(t + 4);
+      }
       if constexpr (kKind == 1) qk(t + 1, sacc, t + 2, CopyOff{});
       vload(t);
 
@@ -519,6 +557,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     // O goes out as whole 1 KB rows: each wave writes its 64 x 64 block (scaled, bf16) into
     // the free ring slots as [row][512] with the 16-byte chunks of row r xor-swizzled by r % 16
     // (two-way bank conflicts at most), then stores 8 rows with 16 contiguous bytes per lane.
+    // (Decode keeps direct stores: measured faster there.)
     DMLA_LDS char* ost = lds;
 #pragma unroll
     for (int qg = 0; qg < 4; ++qg) {
@@ -633,7 +672,6 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
     const int t0 = r * T, t1 = min(t0 + T, total);
     if (t0 >= t1) return;
     const MqaParams* params = (const MqaParams*)(__builtin_amdgcn_kernarg_segment_ptr());
-    DMLA_LDS int* page_cache = reinterpret_cast<DMLA_LDS int*>(lds + kPageOffset);
     for (int bseq = range_first_b[r]; bseq < p.B; ++bseq) {
       const int tb = tile_prefix[bseq];
       if (tb >= t1) break;
@@ -648,11 +686,6 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
       wk.nsplit = num_splits[bseq];
       wk.split = r - tb / T;
       wk.slot = split_base[bseq] + wk.split;
-      const int page_end = (wk.tile_end + (kPage / kTileN) - 1) / (kPage / kTileN);
-      // Cache this segment's page indices in LDS (read by the wave-uniform staging code).
-      for (int i = threadIdx.x; i < page_end - wk.page_begin; i += kThreads)
-        page_cache[i] = p.block_table[bseq * p.bt_sb + wk.page_begin + i];
-      __syncthreads();
       if (((wave >> 1) & 1) == 0) mqa_fwd_body<kDecode, 0, false>(p, params, wk, lds, wave, lane);
       else mqa_fwd_body<kDecode, 1, false>(p, params, wk, lds, wave, lane);
       __syncthreads();   // every LDS read of this segment is done before the next one's copies
