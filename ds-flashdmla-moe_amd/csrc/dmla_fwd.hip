@@ -117,17 +117,23 @@ struct Work {
 };
 
 // ---- decode plan --------------------------------------------------------------------------
-// The key tiles (32 tokens) of all sequences, in order, are cut into R ranges of T tiles each
-// (T = ceil(total / R)); range r is processed by head_groups workgroups on one XCD, one per
-// group of 64 heads, so every workgroup gets the same number of tiles whatever the context
-// lengths.  A range may span several sequences: each piece is one split of its sequence, and
-// sequences with more than one split are merged by the LSE combine.
-// Layout (int32): header[8] = {B, R, T, total tiles, total splits, 0, 0, 0}, then
+// The key tiles (32 tokens) of all sequences, in order, are cut into R ranges; range r is
+// processed by head_groups workgroups on one XCD, one per group of 64 heads.  Every piece of
+// a sequence in a range is one split of that sequence (a segment of the workgroup's work);
+// sequences with more than one split are merged by the LSE combine.  A segment costs a fixed
+// prologue and epilogue (loading Q and the first tile, writing the output) of about
+// kSegCost tiles, so the ranges are equal in the weighted space where each nonempty sequence
+// is preceded by kSegCost virtual tiles: range r starts at weighted position r W with
+// W = ceil(weighted total / R), moved to the sequence's first tile when it falls among the
+// virtual ones.  The work per workgroup is then about the same whatever the context lengths.
+// Layout (int32): header[8] = {B, R, W, total tiles, total splits, kSegCost, 0, 0}, then
 // tile_prefix[B + 1], split_base[B + 1] (first partial slot of each sequence), num_splits[B],
-// range_first_b[R] (the sequence containing the range's first tile).
+// first_range[B], range_start[R + 1] (first tile of each range, in the concatenated tile
+// space), range_first_b[R] (the sequence holding the range's first tile).
 constexpr int kPlanHeader = 8;
+constexpr int kSegCost = 16;                          // measured: ~18 us per segment, ~1.1 us per tile
 constexpr int kMaxSegTiles = 2 * kMaxSegPages - 2;   // a segment's pages fit its page registers
-__host__ __device__ inline int64_t plan_ints(int64_t B, int64_t R) { return kPlanHeader + 3 * B + 2 + R; }
+__host__ __device__ inline int64_t plan_ints(int64_t B, int64_t R) { return kPlanHeader + 4 * B + 2 + 2 * R + 1; }
 
 template <bool kDecode, int kHalf>
 __device__ __noinline__ void mqa_fwd_exact(const MqaParams* params, Work wk, DMLA_LDS char* lds, int wave, int lane);
@@ -664,12 +670,13 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
     const int r = (id / (8 * p.head_groups)) * 8 + id % 8;
     if (r >= p.n_ranges) return;
     const int32_t* plan = p.plan;
-    const int T = plan[2], total = plan[3];
     const int32_t* tile_prefix = plan + kPlanHeader;
     const int32_t* split_base = tile_prefix + p.B + 1;
     const int32_t* num_splits = split_base + p.B + 1;
-    const int32_t* range_first_b = num_splits + p.B;
-    const int t0 = r * T, t1 = min(t0 + T, total);
+    const int32_t* first_range = num_splits + p.B;
+    const int32_t* range_start = first_range + p.B;
+    const int32_t* range_first_b = range_start + p.n_ranges + 1;
+    const int t0 = range_start[r], t1 = range_start[r + 1];
     if (t0 >= t1) return;
     const MqaParams* params = (const MqaParams*)(__builtin_amdgcn_kernarg_segment_ptr());
     for (int bseq = range_first_b[r]; bseq < p.B; ++bseq) {
@@ -684,7 +691,7 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
       wk.tile_end = seg1 - tb;
       wk.page_begin = wk.tile_begin / (kPage / kTileN);
       wk.nsplit = num_splits[bseq];
-      wk.split = r - tb / T;
+      wk.split = r - first_range[bseq];
       wk.slot = split_base[bseq] + wk.split;
       if (((wave >> 1) & 1) == 0) mqa_fwd_body<kDecode, 0, false>(p, params, wk, lds, wave, lane);
       else mqa_fwd_body<kDecode, 1, false>(p, params, wk, lds, wave, lane);
@@ -700,7 +707,9 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlen
   int32_t* tile_prefix = plan + kPlanHeader;
   int32_t* split_base = tile_prefix + B + 1;
   int32_t* num_splits = split_base + B + 1;
-  int32_t* range_first_b = num_splits + B;
+  int32_t* first_range = num_splits + B;
+  int32_t* range_start = first_range + B;
+  int32_t* range_first_b = range_start + R + 1;
   const int tid = threadIdx.x;
   // Exclusive prefix over 1024-element chunks: Hillis-Steele within the chunk plus a carry.
   auto chunk_scan = [&](int v) -> int {   // returns the inclusive scan; scan[1023] is the total
@@ -714,7 +723,9 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlen
     }
     return scan[tid];
   };
-  int carry = 0;
+  // tile_prefix, and the count of nonempty sequences before each one (kept in num_splits for
+  // now: the weighted start of sequence b is tile_prefix[b] + kSegCost * nonempty_before[b]).
+  int carry = 0, ncarry = 0;
   for (int base = 0; base < B; base += 1024) {
     const int b = base + tid;
     int nt = 0;
@@ -723,21 +734,60 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlen
     if (b < B) tile_prefix[b] = carry + incl - nt;
     carry += scan[1023];
     __syncthreads();
+    const int ne = nt > 0 ? 1 : 0;
+    const int incl2 = chunk_scan(ne);
+    if (b < B) num_splits[b] = ncarry + incl2 - ne;
+    ncarry += scan[1023];
+    __syncthreads();
   }
   const int total = carry;
-  const int T = max(1, (total + R - 1) / R);
+  const int64_t weighted = (int64_t)total + (int64_t)kSegCost * ncarry;
+  const int W = (int)max<int64_t>(1, (weighted + R - 1) / R);
   if (tid == 0) tile_prefix[B] = total;
   __threadfence_block();
   __syncthreads();
+  // Range starts: weighted position r W -> the sequence holding it (last b whose weighted start
+  // is <= it) -> its tile, or the sequence's first tile when among its virtual tiles.
+  for (int r = tid; r <= R; r += 1024) {
+    int t = total;
+    if (r < R && (int64_t)r * W < weighted) {
+      const int64_t pos = (int64_t)r * W;
+      int lo = 0, hi = B - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if ((int64_t)tile_prefix[mid] + (int64_t)kSegCost * num_splits[mid] <= pos) lo = mid; else hi = mid - 1;
+      }
+      const int64_t off = pos - ((int64_t)tile_prefix[lo] + (int64_t)kSegCost * num_splits[lo]);
+      t = tile_prefix[lo] + (int)max<int64_t>(0, off - kSegCost);
+      t = min(t, tile_prefix[lo + 1]);
+    }
+    range_start[r] = t;
+  }
+  __threadfence_block();
+  __syncthreads();
+  // first_range[b] / last range: the last range starting at or before the sequence's first /
+  // last tile; num_splits and split_base follow.
+  auto range_of = [&](int t) {
+    int lo = 0, hi = R - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) / 2;
+      if (range_start[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+  };
   int scarry = 0;
   for (int base = 0; base < B; base += 1024) {
     const int b = base + tid;
-    int ns = 0;
+    int ns = 0, fr = 0;
     if (b < B) {
       const int tb = tile_prefix[b], te = tile_prefix[b + 1];
-      ns = te > tb ? (te - 1) / T - tb / T + 1 : 0;
-      num_splits[b] = ns;
+      if (te > tb) {
+        fr = range_of(tb);
+        ns = range_of(te - 1) - fr + 1;
+      }
     }
+    __syncthreads();   // every thread has read num_splits (the nonempty counts) before the writes
+    if (b < B) { num_splits[b] = ns; first_range[b] = fr; }
     const int incl = chunk_scan(ns);
     if (b < B) split_base[b] = scarry + incl - ns;
     scarry += scan[1023];
@@ -745,13 +795,12 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlen
   }
   if (tid == 0) {
     split_base[B] = scarry;
-    plan[0] = B; plan[1] = R; plan[2] = T; plan[3] = total; plan[4] = scarry;
-    plan[5] = plan[6] = plan[7] = 0;
+    plan[0] = B; plan[1] = R; plan[2] = W; plan[3] = total; plan[4] = scarry; plan[5] = kSegCost;
+    plan[6] = plan[7] = 0;
   }
-  // range_first_b[r]: the last sequence b with tile_prefix[b] <= r T and a nonempty span
-  // there (binary search for the last b with tile_prefix[b] <= r T).
+  // range_first_b[r]: the sequence holding tile range_start[r] (last b with tile_prefix[b] <= it)
   for (int r = tid; r < R; r += 1024) {
-    const int t = r * T;
+    const int t = range_start[r];
     int lo = 0, hi = B - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) / 2;

@@ -124,13 +124,17 @@ int dmla_decode_paged(const void* q, const void* kv_pool, const int32_t* block_t
 /*
  * Decode tile-scheduler plan, computed on the device from cache_seqlens (no reference
  * counterpart; the step between the block table and the decode kernel).  The 32-token key
- * tiles of all sequences, in order, are cut into R equal ranges (R = CUs / head groups of 64
- * heads, more if one range's pages would exceed 1024), each processed by one workgroup per
- * head group, so the work per workgroup does not depend on how the lengths are distributed.
- * A range that spans sequences contributes one split to each; sequences with several splits
- * are merged by the LSE combine.  plan (int32, dmla_decode_plan_bytes bytes):
- *   [0..7]   B, R, T (tiles per range), total tiles, total splits, 0, 0, 0
- *   then     tile_prefix[B + 1], split_base[B + 1], num_splits[B], range_first_b[R]
+ * tiles of all sequences, in order, are cut into R ranges (R = CUs / head groups of 64 heads,
+ * more if a range's pages could exceed 128), each processed by one workgroup per head group.
+ * Every piece of a sequence inside a range is one split of it (a segment of the workgroup's
+ * work); sequences with several splits are merged by the LSE combine.  A segment has a fixed
+ * cost (loading Q and its first tile, writing its output) of about 16 tiles, so the ranges are
+ * equal in a weighted space where each nonempty sequence is preceded by 16 virtual tiles:
+ * every workgroup gets about the same work whatever the lengths.  plan (int32,
+ * dmla_decode_plan_bytes bytes):
+ *   [0..7]   B, R, W (weighted tiles per range), total tiles, total splits, segment cost, 0, 0
+ *   then     tile_prefix[B + 1], split_base[B + 1], num_splits[B], first_range[B],
+ *            range_start[R + 1], range_first_b[R]
  * A plan depends on cache_seqlens only, so one plan serves every layer of a decode step.
  */
 int64_t dmla_decode_plan_bytes(int64_t B, int64_t H, int64_t max_pages_per_seq);

@@ -183,25 +183,55 @@ def dmla_decode_paged(q: Tensor, kv_pool: Tensor, block_table: Tensor, cache_seq
     return torch.stack(outs), torch.stack(lses)
 
 
-def decode_plan(cache_seqlens, n_ranges: int, max_pages: int, page_size: int = 64, tile: int = 32):
-    """The decode tile-scheduler plan for R = n_ranges (no reference counterpart): 32-token
-    tiles of all sequences in order, cut into R ranges of T = ceil(total / R) tiles (T >= 1).
-    Returns the int32 list header[8] + tile_prefix[B+1] + split_base[B+1] + num_splits[B] +
-    range_first_b[R] with the layout of include/flashdmla.h."""
-    B = len(cache_seqlens)
+def decode_plan(cache_seqlens, n_ranges: int, max_pages: int, page_size: int = 64, tile: int = 32,
+                seg_cost: int = 16):
+    """The decode tile-scheduler plan for R = n_ranges (no reference counterpart).
+
+    The 32-token tiles of all sequences, in order, are cut into R ranges that are equal in a
+    weighted space where every nonempty sequence is preceded by seg_cost virtual tiles (the
+    fixed cost of a segment): range r starts at weighted position r*W, W = ceil(weighted/R),
+    which maps to the tile at that position, or to the sequence's first tile when the position
+    is among its virtual tiles.  Returns the int32 list header[8] + tile_prefix[B+1] +
+    split_base[B+1] + num_splits[B] + first_range[B] + range_start[R+1] + range_first_b[R]
+    with the layout of include/flashdmla.h."""
+    B, R = len(cache_seqlens), n_ranges
     tiles = [(min(max(int(x), 0), max_pages * page_size) + tile - 1) // tile for x in cache_seqlens]
     tp = [0]
     for n in tiles:
         tp.append(tp[-1] + n)
     total = tp[-1]
-    T = max(1, -(-total // n_ranges))
-    ns = [(tp[b + 1] - 1) // T - tp[b] // T + 1 if tp[b + 1] > tp[b] else 0 for b in range(B)]
+    wstart, ne = [], 0          # weighted start of each sequence
+    for b in range(B):
+        wstart.append(tp[b] + seg_cost * ne)
+        ne += tiles[b] > 0
+    weighted = total + seg_cost * ne
+    W = max(1, -(-weighted // R))
+    rs = []
+    for r in range(R):
+        pos = r * W
+        if pos >= weighted:
+            rs.append(total)
+            continue
+        b = max(i for i in range(B) if wstart[i] <= pos)
+        rs.append(min(tp[b] + max(0, pos - wstart[b] - seg_cost), tp[b + 1]))
+    rs.append(total)
+
+    def range_of(t):
+        return max(r for r in range(R) if rs[r] <= t)
+
+    ns, fr = [], []
+    for b in range(B):
+        if tiles[b]:
+            fr.append(range_of(tp[b]))
+            ns.append(range_of(tp[b + 1] - 1) - fr[-1] + 1)
+        else:
+            fr.append(0)
+            ns.append(0)
     sb = [0]
     for n in ns:
         sb.append(sb[-1] + n)
-    # the sequence holding tile r*T: the last b with tile_prefix[b] <= r*T
-    rfb = [max(b for b in range(B) if tp[b] <= r * T) for r in range(n_ranges)]
-    return [B, n_ranges, T, total, sb[-1], 0, 0, 0] + tp + sb + ns + rfb
+    rfb = [max(b for b in range(B) if tp[b] <= rs[r]) for r in range(R)]
+    return [B, R, W, total, sb[-1], seg_cost, 0, 0] + tp + sb + ns + fr + rs + rfb
 
 
 def kv_append(kv_pool: Tensor, block_table: Tensor, cache_seqlens: Tensor, new_kv: Tensor,

@@ -284,22 +284,20 @@ def test_lse_combine_of_key_splits_is_full_attention():
 
 
 # ---------------------------------------------------------------- decode plan
-@pytest.mark.parametrize("lens,nr", [([5, 0, 70, 1, 64, 0], 4), ([1000, 3000, 10, 8192], 16), ([0, 0], 3), ([33], 8)])
-def test_decode_plan_covers_every_tile_once(lens, nr):
-    max_pages = 128
-    plan = R.decode_plan(lens, nr, max_pages)
+def _walk_plan(plan, lens):
+    """Walks the ranges like the decode kernel; returns {(b, tile): range} and splits per b."""
     B = len(lens)
-    hdr, tp = plan[:8], plan[8:8 + B + 1]
+    hdr = plan[:8]
+    tp = plan[8:8 + B + 1]
     sb = plan[8 + B + 1:8 + 2 * (B + 1)]
-    ns = plan[8 + 2 * (B + 1):8 + 2 * (B + 1) + B]
-    rfb = plan[8 + 2 * (B + 1) + B:]
-    assert hdr[0] == B and hdr[1] == nr and len(rfb) == nr
-    T, total = hdr[2], hdr[3]
-    assert total == sum((x + 31) // 32 for x in lens) and T == max(1, -(-total // nr))
-    # walk the ranges like the decode kernel: every (sequence, tile) exactly once, splits counted
-    seen, splits = {}, [0] * B
+    o = 8 + 2 * (B + 1)
+    ns, fr = plan[o:o + B], plan[o + B:o + 2 * B]
+    nr = hdr[1]
+    rs = plan[o + 2 * B:o + 2 * B + nr + 1]
+    rfb = plan[o + 2 * B + nr + 1:o + 2 * B + 2 * nr + 1]
+    seen, splits, segs = {}, [0] * B, [0] * nr
     for r in range(nr):
-        t0, t1 = r * T, min(r * T + T, total)
+        t0, t1 = rs[r], rs[r + 1]
         if t0 >= t1:
             continue
         b = rfb[r]
@@ -307,14 +305,39 @@ def test_decode_plan_covers_every_tile_once(lens, nr):
         while b < B and tp[b] < t1:
             s0, s1 = max(t0, tp[b]), min(t1, tp[b + 1])
             if s0 < s1:
-                assert r - tp[b] // T == splits[b]          # split index = order of the pieces
+                assert r - fr[b] == splits[b]          # split index = order of the pieces
                 splits[b] += 1
+                segs[r] += 1
                 for t in range(s0, s1):
                     assert (b, t - tp[b]) not in seen
                     seen[(b, t - tp[b])] = r
             b += 1
-    assert len(seen) == total
+    return hdr, tp, sb, ns, rs, seen, splits, segs
+
+
+@pytest.mark.parametrize("lens,nr", [([5, 0, 70, 1, 64, 0], 4), ([1000, 3000, 10, 8192], 16), ([0, 0], 3),
+                                     ([33], 8), ([7] * 50, 8), ([3000] + [1] * 30, 5)])
+def test_decode_plan_covers_every_tile_once(lens, nr):
+    plan = R.decode_plan(lens, nr, 128)
+    hdr, tp, sb, ns, rs, seen, splits, segs = _walk_plan(plan, lens)
+    B = len(lens)
+    assert hdr[0] == B and hdr[1] == nr and hdr[5] == 16
+    total = sum((x + 31) // 32 for x in lens)
+    assert hdr[3] == total and len(seen) == total and rs[0] == 0 and rs[-1] == total
+    assert all(rs[i] <= rs[i + 1] for i in range(nr))
     assert splits == ns and sb == [sum(ns[:i]) for i in range(B + 1)] and hdr[4] == sum(ns)
+
+
+def test_decode_plan_balances_tiles_plus_segment_costs():
+    # BASELINE config 3 shape: 64 contexts in [1024, 8192], 128 ranges
+    g = torch.Generator().manual_seed(3)
+    lens = torch.randint(1024, 8193, (64,), generator=g).tolist()
+    plan = R.decode_plan(lens, 128, 128)
+    hdr, tp, sb, ns, rs, seen, splits, segs = _walk_plan(plan, lens)
+    W = hdr[2]
+    cost = [(rs[r + 1] - rs[r]) + 16 * segs[r] for r in range(128)]
+    # every range's weighted cost is within one segment cost of W (the first segment included)
+    assert max(cost) <= W + 16 and min(c for c in cost if c) >= W - 16 - 16
 
 
 def test_attention_with_no_keys_is_the_fully_masked_case():
