@@ -700,50 +700,76 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
   }
 }
 
-// One workgroup computes the decode plan (layout above) from the context lengths.
+// One workgroup computes the decode plan (layout above) from the context lengths.  The arrays
+// the binary searches read are mirrored in LDS when they fit (the common case), so every
+// dependent step is an LDS access rather than a global memory round trip.
+constexpr int kPlanLds = 4096;
 __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlens, int B, int R, int max_pages,
                                                            int32_t* plan) {
   __shared__ int scan[1024];
+  __shared__ int l_tp[kPlanLds], l_ne[kPlanLds], l_rs[kPlanLds];
   int32_t* tile_prefix = plan + kPlanHeader;
   int32_t* split_base = tile_prefix + B + 1;
   int32_t* num_splits = split_base + B + 1;
   int32_t* first_range = num_splits + B;
   int32_t* range_start = first_range + B;
   int32_t* range_first_b = range_start + R + 1;
+  const bool lds_b = B + 1 <= kPlanLds, lds_r = R + 1 <= kPlanLds;
+  // nonempty_before[b] lives in num_splits until the split counts replace it
+  const int* tp = lds_b ? l_tp : tile_prefix;
+  const int* ne = lds_b ? l_ne : num_splits;
+  const int* rs = lds_r ? l_rs : range_start;
   const int tid = threadIdx.x;
-  // Exclusive prefix over 1024-element chunks: Hillis-Steele within the chunk plus a carry.
-  auto chunk_scan = [&](int v) -> int {   // returns the inclusive scan; scan[1023] is the total
-    scan[tid] = v;
-    __syncthreads();
-    for (int off = 1; off < 1024; off *= 2) {
-      const int add = tid >= off ? scan[tid - off] : 0;
-      __syncthreads();
-      scan[tid] += add;
-      __syncthreads();
+  // Prefix over 1024-element chunks: a shuffle scan within each wave, the 16 wave totals
+  // scanned by wave 0 through LDS, two barriers per chunk.  Returns the inclusive scan;
+  // scan[1023] is the chunk total afterwards.
+  auto chunk_scan = [&](int v) -> int {
+    const int ln = tid & 63, wv = tid >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off *= 2) {
+      const int up = __shfl_up(v, off, 64);
+      if (ln >= off) v += up;
     }
-    return scan[tid];
+    if (ln == 63) scan[wv] = v;
+    __syncthreads();
+    if (wv == 0) {
+      int t = ln < 16 ? scan[ln] : 0;
+#pragma unroll
+      for (int off = 1; off < 16; off *= 2) {
+        const int up = __shfl_up(t, off, 64);
+        if (ln >= off) t += up;
+      }
+      if (ln < 16) scan[32 + ln] = t;   // inclusive wave-total prefix
+    }
+    __syncthreads();
+    const int incl = v + (wv > 0 ? scan[32 + wv - 1] : 0);
+    if (tid == 1023) scan[1023] = incl;
+    __syncthreads();
+    return incl;
   };
-  // tile_prefix, and the count of nonempty sequences before each one (kept in num_splits for
-  // now: the weighted start of sequence b is tile_prefix[b] + kSegCost * nonempty_before[b]).
   int carry = 0, ncarry = 0;
   for (int base = 0; base < B; base += 1024) {
     const int b = base + tid;
     int nt = 0;
     if (b < B) nt = (min(max(seqlens[b], 0), max_pages * kPage) + kTileN - 1) / kTileN;
     const int incl = chunk_scan(nt);
-    if (b < B) tile_prefix[b] = carry + incl - nt;
+    const int tpb = carry + incl - nt;
     carry += scan[1023];
     __syncthreads();
-    const int ne = nt > 0 ? 1 : 0;
-    const int incl2 = chunk_scan(ne);
-    if (b < B) num_splits[b] = ncarry + incl2 - ne;
+    const int nz = nt > 0 ? 1 : 0;
+    const int incl2 = chunk_scan(nz);
+    const int neb = ncarry + incl2 - nz;
     ncarry += scan[1023];
+    if (b < B) {
+      tile_prefix[b] = tpb; num_splits[b] = neb;
+      if (lds_b) { l_tp[b] = tpb; l_ne[b] = neb; }
+    }
     __syncthreads();
   }
   const int total = carry;
+  if (tid == 0) { tile_prefix[B] = total; if (lds_b) l_tp[B] = total; }
   const int64_t weighted = (int64_t)total + (int64_t)kSegCost * ncarry;
   const int W = (int)max<int64_t>(1, (weighted + R - 1) / R);
-  if (tid == 0) tile_prefix[B] = total;
   __threadfence_block();
   __syncthreads();
   // Range starts: weighted position r W -> the sequence holding it (last b whose weighted start
@@ -755,13 +781,14 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlen
       int lo = 0, hi = B - 1;
       while (lo < hi) {
         const int mid = (lo + hi + 1) / 2;
-        if ((int64_t)tile_prefix[mid] + (int64_t)kSegCost * num_splits[mid] <= pos) lo = mid; else hi = mid - 1;
+        if ((int64_t)tp[mid] + (int64_t)kSegCost * ne[mid] <= pos) lo = mid; else hi = mid - 1;
       }
-      const int64_t off = pos - ((int64_t)tile_prefix[lo] + (int64_t)kSegCost * num_splits[lo]);
-      t = tile_prefix[lo] + (int)max<int64_t>(0, off - kSegCost);
-      t = min(t, tile_prefix[lo + 1]);
+      const int64_t off = pos - ((int64_t)tp[lo] + (int64_t)kSegCost * ne[lo]);
+      t = tp[lo] + (int)max<int64_t>(0, off - kSegCost);
+      t = min(t, tp[lo + 1]);
     }
     range_start[r] = t;
+    if (lds_r) l_rs[r] = t;
   }
   __threadfence_block();
   __syncthreads();
@@ -771,7 +798,7 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlen
     int lo = 0, hi = R - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) / 2;
-      if (range_start[mid] <= t) lo = mid; else hi = mid - 1;
+      if (rs[mid] <= t) lo = mid; else hi = mid - 1;
     }
     return lo;
   };
@@ -780,13 +807,13 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlen
     const int b = base + tid;
     int ns = 0, fr = 0;
     if (b < B) {
-      const int tb = tile_prefix[b], te = tile_prefix[b + 1];
+      const int tb = tp[b], te = tp[b + 1];
       if (te > tb) {
         fr = range_of(tb);
         ns = range_of(te - 1) - fr + 1;
       }
     }
-    __syncthreads();   // every thread has read num_splits (the nonempty counts) before the writes
+    __syncthreads();   // every thread is past its reads of the nonempty counts
     if (b < B) { num_splits[b] = ns; first_range[b] = fr; }
     const int incl = chunk_scan(ns);
     if (b < B) split_base[b] = scarry + incl - ns;
@@ -800,11 +827,11 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlen
   }
   // range_first_b[r]: the sequence holding tile range_start[r] (last b with tile_prefix[b] <= it)
   for (int r = tid; r < R; r += 1024) {
-    const int t = range_start[r];
+    const int t = rs[r];
     int lo = 0, hi = B - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) / 2;
-      if (tile_prefix[mid] <= t) lo = mid; else hi = mid - 1;
+      if (tp[mid] <= t) lo = mid; else hi = mid - 1;
     }
     range_first_b[r] = lo;
   }
