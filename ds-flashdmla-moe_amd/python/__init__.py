@@ -7,11 +7,13 @@ from .ops import (  # noqa: F401
     FlashDMLAOnTheFly,
     flash_dmla,
     flash_dmla_bwd,
+    flash_dmla_bwd_onthefly,
     flash_dmla_decode_paged,
     flash_dmla_decode_plan,
     flash_dmla_fwd,
     flash_dmla_fwd_onthefly,
     flash_dmla_kv_append,
     flash_dmla_lse_combine,
+    flash_dmla_onthefly,
 )
 from ._lib import DmlaError, DmlaInvalidArgument, DmlaUnsupported  # noqa: F401

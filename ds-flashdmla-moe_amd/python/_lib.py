@@ -98,6 +98,14 @@ SIGNATURES = {
         + [_i64] * 16  # q(3) k(2) o(3) dout(3) dq(3) dk(2) strides
         + [_int, _int, _f32, _int, _ptr, _i64, _ptr],  # dq_fp32 dk_fp32 scale causal ws ws_bytes stream
     ),
+    "dmla_bwd_onthefly_workspace_bytes": (_i64, [_i64] * 6),  # B H Sq Sk d_in d_lat
+    "dmla_bwd_onthefly": (
+        _int,
+        [_ptr] * 14  # q, k, v, wk, wv, o, dout, m, l, dq, dk, dv, dwk, dwv
+        + [_i64] * 6  # B, H, Sq, Sk, d_in, d_lat
+        + [_i64] * 25  # q(3) k(3) v(3) w(2) o(3) dout(3) dq(3) dk(3) dw(2) strides
+        + [_int, _f32, _int, _ptr, _i64, _ptr],  # dw_fp32 scale causal ws ws_bytes stream
+    ),
 }
 
 _lib = None

@@ -376,22 +376,108 @@ def flash_dmla_bwd(
     return dq, dk
 
 
+def flash_dmla_bwd_onthefly(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    wk: torch.Tensor,
+    wv: torch.Tensor,
+    o: torch.Tensor,
+    do: torch.Tensor,
+    m: torch.Tensor,
+    l: torch.Tensor,
+    softmax_scale: Optional[float] = None,
+    causal: bool = True,
+    dw_dtype: torch.dtype = torch.float32,
+    check_range: bool = False,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """On-the-fly DMLA backward from the saved statistics: returns (dq, dk, dv, dwk, dwv).
+
+    Shapes as for flash_dmla_fwd_onthefly; dq [B, H, Sq, 64], dk and dv [B, Sk, H, 128] in
+    bf16; dwk and dwv [H, 128, 64] in dw_dtype (default float32: they sum over every batch
+    element and position, and at config-4 sizes reach ~30, where a bf16 rounding alone is 0.06).
+    m, l must be the forward's statistics (return_stats=True).
+    Every product runs on fp16 operands with q, k, v, do and the weights converted exactly;
+    check_range=True verifies on the host (one device sync) that they stay inside fp16's range.
+    """
+    _check_bf16("q", q, 4)
+    _check_bf16("o", o, 4)
+    _check_bf16("do", do, 4)
+    for name, t in (("k", k), ("v", v)):
+        _check_bf16(name, t, 4)
+    for name, t in (("wk", wk), ("wv", wv)):
+        _check_bf16(name, t, 3)
+    B, H, Sq, Dl = q.shape
+    Sk, Din = k.shape[1], k.shape[3]
+    _require(tuple(k.shape) == (B, Sk, H, Din) and tuple(v.shape) == (B, Sk, H, Din),
+             "k and v must both be [B, Sk, H, d_in] with q's B and H")
+    _require(tuple(wk.shape) == (H, Din, Dl) and tuple(wv.shape) == (H, Din, Dl),
+             "wk and wv must be [H, d_in, d_lat]")
+    _require(wk.stride() == wv.stride(), "wk and wv must share strides")
+    _require(tuple(o.shape) == (B, H, Sq, Dl) and tuple(do.shape) == (B, H, Sq, Dl), "o and do must be [B, H, Sq, d_lat]")
+    for name, t in (("m", m), ("l", l)):
+        _require(t.dtype == torch.float32 and t.is_cuda and t.is_contiguous() and tuple(t.shape) == (B, H, Sq),
+                 f"{name} must be a contiguous float32 GPU tensor [B, H, Sq]")
+    if check_range:
+        for name, t in (("q", q), ("k", k), ("v", v), ("do", do), ("wk", wk), ("wv", wv)):
+            _require(bool(torch.isfinite(t).all()) and float(t.abs().max()) <= 65504.0,
+                     f"{name} has entries outside fp16's finite range (|x| <= 65504)")
+    dq = torch.empty((B, H, Sq, Dl), dtype=torch.bfloat16, device=q.device)
+    dk = torch.empty((B, Sk, H, Din), dtype=torch.bfloat16, device=q.device)
+    dv = torch.empty_like(dk)
+    _require(dw_dtype in (torch.bfloat16, torch.float32), "dw_dtype must be bfloat16 or float32")
+    dwk = torch.empty((H, Din, Dl), dtype=dw_dtype, device=q.device)
+    dwv = torch.empty_like(dwk)
+    if B * H == 0:
+        return dq, dk, dv, dwk, dwv
+    if Sq == 0 or Sk == 0:   # nothing attends: every gradient is zero
+        return dq.zero_(), dk.zero_(), dv.zero_(), dwk.zero_(), dwv.zero_()
+    ws_bytes = int(_lib.lib().dmla_bwd_onthefly_workspace_bytes(B, H, Sq, Sk, Din, Dl))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
+    _lib.call(
+        "dmla_bwd_onthefly",
+        _ptr(q), _ptr(k), _ptr(v), _ptr(wk), _ptr(wv), _ptr(o), _ptr(do), _ptr(m), _ptr(l),
+        _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dwk), _ptr(dwv),
+        B, H, Sq, Sk, Din, Dl,
+        q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
+        v.stride(0), v.stride(1), v.stride(2), wk.stride(0), wk.stride(1),
+        o.stride(0), o.stride(1), o.stride(2), do.stride(0), do.stride(1), do.stride(2),
+        dq.stride(0), dq.stride(1), dq.stride(2), dk.stride(0), dk.stride(1), dk.stride(2),
+        dwk.stride(0), dwk.stride(1), 1 if dw_dtype == torch.float32 else 0,
+        _scale(softmax_scale, Dl), 1 if causal else 0, _ptr(ws), ws_bytes, _stream(q),
+    )
+    return dq, dk, dv, dwk, dwv
+
+
 class FlashDMLAOnTheFly(torch.autograd.Function):
     """o = FlashDMLAOnTheFly.apply(q, k, v, wk, wv, softmax_scale, causal).
 
-    Forward only: the gradients of the on-the-fly mode (dq, dk, dv, dwk, dwv) are not built
-    into this library, and backward raises instead of returning something approximate.
+    Saves q, k, v, wk, wv, o and the row statistics m, l; backward(do) returns the gradients
+    of q, k, v, wk and wv (flash_dmla_bwd_onthefly; the weight gradients are summed in fp32 and
+    cast to the weights' dtype by autograd).
     """
 
     @staticmethod
     def forward(ctx, q, k, v, wk, wv, softmax_scale=None, causal=True):
-        return flash_dmla_fwd_onthefly(q, k, v, wk, wv, softmax_scale, causal)
+        o, m, l = flash_dmla_fwd_onthefly(q, k, v, wk, wv, softmax_scale, causal, return_stats=True)
+        ctx.save_for_backward(q, k, v, wk, wv, o, m, l)
+        ctx.softmax_scale = softmax_scale
+        ctx.causal = causal
+        return o
 
     @staticmethod
     def backward(ctx, do):
-        raise NotImplementedError("FlashDMLAOnTheFly: the on-the-fly backward is not built into this library")
+        q, k, v, wk, wv, o, m, l = ctx.saved_tensors
+        dq, dk, dv, dwk, dwv = flash_dmla_bwd_onthefly(q, k, v, wk, wv, o, do.contiguous(), m, l,
+                                                       ctx.softmax_scale, ctx.causal)
+        return dq, dk, dv, dwk, dwv, None, None
 
 
 def flash_dmla(q, k_lat, d_v=D_V, softmax_scale=None, causal=True):
     """Differentiable cache-latent DMLA attention (functional form of FlashDMLACacheLatent)."""
     return FlashDMLACacheLatent.apply(q, k_lat, d_v, softmax_scale, causal)
+
+
+def flash_dmla_onthefly(q, k, v, wk, wv, softmax_scale=None, causal=True):
+    """Differentiable on-the-fly DMLA attention (functional form of FlashDMLAOnTheFly)."""
+    return FlashDMLAOnTheFly.apply(q, k, v, wk, wv, softmax_scale, causal)

@@ -78,7 +78,7 @@ int dmla_fwd_cache_latent(const void* q, const void* k_lat, void* o, float* m, f
  *   o      [B, H, Sq, d_lat]   bf16  strides (o_sb, o_sh, o_ss)
  *   m, l   [B, H, Sq]          fp32  contiguous; may both be NULL
  *
- *   K_lat[b,h] = k[b,:,h,:] wk[h] and V_lat[b,h] = v[b,:,h,:] wv[h] (rounded to bf16 inside
+ *   K_lat[b,h] = k[b,:,h,:] wk[h] and V_lat[b,h] = v[b,:,h,:] wv[h] (rounded to fp16 inside
  *   the kernel), then o = softmax(softmax_scale q K_lat^T (+ causal mask)) V_lat with the
  *   statistics of dmla_fwd_cache_latent (natural-log units; m = -inf, l = 0, o = 0 for a row
  *   without an unmasked key).  causal != 0 masks key j > i + (Sk - Sq).
@@ -232,6 +232,46 @@ int dmla_bwd_cache_latent(const void* q, const void* k_lat, const void* o, const
                           int64_t dk_sb, int64_t dk_ss, int dq_fp32, int dk_fp32,
                           float softmax_scale, int causal, void* workspace,
                           int64_t workspace_bytes, dmla_stream_t stream);
+
+/*
+ * On-the-fly DMLA backward from the forward's saved statistics.
+ * Replaces: fa2_backward (csrc/attention/fa2_bwd.cu:319-356, math of :198-310) in the
+ * on-the-fly mode of README.md:14, whose WK / WV are learnable -- the role of the absent
+ * csrc/attention/fa2_dmla_bwd.cu (README.md:46) for that mode.  The reference has no code for
+ * it; the gradients are those of dmla_fwd_onthefly's math.
+ *
+ *   q, k, v, wk, wv, o  as for dmla_fwd_onthefly (o is the forward's output)
+ *   dout   [B, H, Sq, d_lat]  bf16  strides (do_sb, do_sh, do_ss)
+ *   m, l   [B, H, Sq]         fp32  contiguous, exactly as dmla_fwd_onthefly wrote them
+ *   dq     [B, H, Sq, d_lat]  bf16  strides (dq_sb, dq_sh, dq_ss)
+ *   dk, dv [B, Sk, H, d_in]   bf16  strides (dk_sb, dk_ss, dk_sh), shared by both
+ *   dwk, dwv [H, d_in, d_lat] bf16, or fp32 when dw_fp32 != 0; strides (dw_sh, dw_si, 1),
+ *                             shared by both
+ *
+ *   With K_lat, V_lat recomputed as in the forward, P = exp(s - m) / l, D_i = sum dout_i o_i,
+ *   dS = P * (dP - D) with dP = dout V_lat^T:
+ *     dq = scale dS K_lat,  dK_lat = scale dS^T q,  dV_lat = P^T dout,
+ *     dk[b,:,h,:] = dK_lat[b,h] wk[h]^T,  dwk[h] = sum_b k[b,:,h,:]^T dK_lat[b,h]  (same for v).
+ *   Rows with l = 0 contribute nothing.  Every product takes fp16 operands with fp32
+ *   accumulation (inputs converted exactly for magnitudes in fp16's normal range; P, dS,
+ *   dK_lat and dV_lat rounded to fp16).  Deterministic (no atomics).  workspace: device memory
+ *   of at least dmla_bwd_onthefly_workspace_bytes(...) bytes, 16-byte aligned; its contents on
+ *   entry do not matter.
+ * Supported: d_in = 128, d_lat = 64, 0 < Sq, Sk <= 2^24.
+ */
+int64_t dmla_bwd_onthefly_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk,
+                                          int64_t d_in, int64_t d_lat);
+int dmla_bwd_onthefly(const void* q, const void* k, const void* v, const void* wk,
+                      const void* wv, const void* o, const void* dout, const float* m,
+                      const float* l, void* dq, void* dk, void* dv, void* dwk, void* dwv,
+                      int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t d_in, int64_t d_lat,
+                      int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t k_sb, int64_t k_ss,
+                      int64_t k_sh, int64_t v_sb, int64_t v_ss, int64_t v_sh, int64_t w_sh,
+                      int64_t w_si, int64_t o_sb, int64_t o_sh, int64_t o_ss, int64_t do_sb,
+                      int64_t do_sh, int64_t do_ss, int64_t dq_sb, int64_t dq_sh, int64_t dq_ss,
+                      int64_t dk_sb, int64_t dk_ss, int64_t dk_sh, int64_t dw_sh, int64_t dw_si,
+                      int dw_fp32, float softmax_scale, int causal, void* workspace,
+                      int64_t workspace_bytes, dmla_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -20,6 +20,9 @@ whose math this module restates in PyTorch eager (fp32 by default, fp64 for pinn
     dS = P*(dP - D), dV = P^T dO, dK = dS^T Q, dQ = dS K), with the softmax scale applied to
     dQ/dK (missing at fa2_bwd.cu:251-254, :306-309) and the statistics taken from the forward
     (README.md:12) instead of recomputed                               -> dmla_bwd_cache_latent
+  * the same backward in the on-the-fly mode, through the projections K WK, V WV to the
+    gradients of K, V, WK and WV (README.md:14 makes WK / WV learnable)
+                                                                        -> dmla_bwd_onthefly
   * paged decode (no reference counterpart): contiguous attention over the
     tokens gathered through the block table                           -> dmla_decode_paged
   * the paged-cache append that produces those pages and the split-KV LSE combine (no
@@ -308,6 +311,48 @@ def dmla_bwd_cache_latent(q: Tensor, k_lat: Tensor, o: Tensor, do: Tensor, m: Te
         dqs.append(dq)
         dks.append(dk)
     return torch.stack(dqs), torch.stack(dks)
+
+
+def dmla_bwd_onthefly(q: Tensor, k: Tensor, v: Tensor, wk: Tensor, wv: Tensor, o: Tensor, do: Tensor,
+                      m: Tensor, l: Tensor, scale: Optional[float] = None, causal: bool = True,
+                      dtype: torch.dtype = torch.float32) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """On-the-fly DMLA backward from the saved statistics (fa2_bwd.cu:198-310 corrected, plus
+    the projection gradients that README.md:14's learnable WK / WV imply).
+
+    K_lat = K WK, V_lat = V WV per head; P = exp(scale*q.K_lat - m) / l, D = rowsum(dO * O),
+    dS = P * (dP - D) with dP = dO V_lat^T; dQ = scale dS K_lat, dK_lat = scale dS^T Q,
+    dV_lat = P^T dO; dK[b,s,h] = dK_lat[b,h,s] WK[h]^T, dWK[h] = sum_{b,s} K[b,s,h]^T dK_lat[b,h,s]
+    (same for V / WV).  Returns (dq, dk, dv, dwk, dwv) in `dtype`.
+    """
+    scale = default_scale(q.shape[-1]) if scale is None else scale
+    q, k, v, wk, wv = (t.to(dtype) for t in (q, k, v, wk, wv))
+    o, do, m, l = o.to(dtype), do.to(dtype), m.to(dtype), l.to(dtype)
+    k_lat, v_lat = project_latent(k, wk), project_latent(v, wv)            # [B, H, Sk, d_lat]
+    s = masked_scores(q, k_lat, scale, causal)
+    m_safe = torch.where(torch.isfinite(m), m, torch.zeros_like(m))
+    inv_l = torch.where(l > 0, 1.0 / l, torch.zeros_like(l))
+    p = torch.exp(s - m_safe.unsqueeze(-1)) * inv_l.unsqueeze(-1)
+    delta = (do * o).sum(dim=-1)
+    dp = torch.matmul(do, v_lat.transpose(-1, -2).contiguous())
+    ds = p * (dp - delta.unsqueeze(-1))
+    dq = scale * torch.matmul(ds, k_lat)
+    dk_lat = scale * torch.matmul(ds.transpose(-1, -2).contiguous(), q)
+    dv_lat = torch.matmul(p.transpose(-1, -2).contiguous(), do)
+    dk = torch.einsum("bhsl,hdl->bshd", dk_lat, wk)
+    dv = torch.einsum("bhsl,hdl->bshd", dv_lat, wv)
+    dwk = torch.einsum("bshd,bhsl->hdl", k, dk_lat)
+    dwv = torch.einsum("bshd,bhsl->hdl", v, dv_lat)
+    return dq, dk, dv, dwk, dwv
+
+
+def dmla_grads_onthefly_autograd(q: Tensor, k: Tensor, v: Tensor, wk: Tensor, wv: Tensor, do: Tensor,
+                                 scale: Optional[float] = None, causal: bool = True,
+                                 dtype: torch.dtype = torch.float64) -> Tuple[Tensor, ...]:
+    """(dq, dk, dv, dwk, dwv) of sum(o * do) by torch.autograd through the exact on-the-fly forward."""
+    xs = [t.detach().to(dtype).requires_grad_(True) for t in (q, k, v, wk, wv)]
+    o, _, _ = dmla_fwd_onthefly(*xs, scale, causal, dtype)
+    (o * do.to(dtype)).sum().backward()
+    return tuple(t.grad for t in xs)
 
 
 def dmla_grads_autograd(q: Tensor, k_lat: Tensor, do: Tensor, d_v: int, scale: Optional[float] = None,

@@ -172,3 +172,48 @@ def test_kv_append_and_combine_argument_errors():
     assert combine(S=0) == _lib.DMLA_ERR_INVALID_ARG
     assert combine(d=6) == _lib.DMLA_ERR_UNSUPPORTED
     assert combine(B=0) == _lib.DMLA_OK
+
+
+def test_onthefly_bwd_workspace_query_and_argument_errors():
+    lib = _lib.lib()
+    P = ctypes.c_void_p
+    need = lib.dmla_bwd_onthefly_workspace_bytes(2, 4, 100, 300, 128, 64)
+    assert need > 0 and need % 256 == 0
+    # K_lat, V_lat, dK_lat, dV_lat as fp16 for every padded key, q and dO as fp16 per padded row
+    assert need >= 4 * 2 * 4 * 384 * 64 * 2 + 2 * 2 * 4 * 128 * 64 * 2
+    assert lib.dmla_bwd_onthefly_workspace_bytes(2, 4, 100, 300, 64, 64) == 0      # unsupported d_in
+    assert lib.dmla_bwd_onthefly_workspace_bytes(0, 4, 100, 300, 128, 64) == 0     # empty problem
+    assert lib.dmla_bwd_onthefly_workspace_bytes(1, 1, 1 << 25, 8, 128, 64) == 0   # above 2^24
+
+    def call(ws_short=256, **kw):
+        a = dict(q=1 << 20, dq=1 << 20, m=1 << 20, B=1, H=2, Sq=64, Sk=64, din=128, dlat=64, scale=0.125, ks=2 * 128,
+                 ws=1 << 20)
+        a.update(kw)
+        ok = lib.dmla_bwd_onthefly_workspace_bytes(a["B"], a["H"], a["Sq"], a["Sk"], 128, 64)
+        ptrs = [P(a["q"])] + [P(1 << 20)] * 6 + [P(a["m"]), P(1 << 20), P(a["dq"])] + [P(1 << 20)] * 4
+        return lib.dmla_bwd_onthefly(
+            *ptrs, a["B"], a["H"], a["Sq"], a["Sk"], a["din"], a["dlat"],
+            2 * 64 * 64, 64 * 64, 64, 64 * a["ks"], a["ks"], 128, 64 * a["ks"], a["ks"], 128, 128 * 64, 64,
+            2 * 64 * 64, 64 * 64, 64, 2 * 64 * 64, 64 * 64, 64, 2 * 64 * 64, 64 * 64, 64,
+            64 * 256, 256, 128, 128 * 64, 64, 1, a["scale"], 1, P(a["ws"]), max(ok - ws_short, 0), None)
+
+    assert call() == _lib.DMLA_ERR_WORKSPACE                         # 256 bytes short
+    assert b"workspace" in lib.dmla_last_error()
+    assert call(q=None) == _lib.DMLA_ERR_INVALID_ARG
+    assert call(dq=(1 << 20) + 2) == _lib.DMLA_ERR_INVALID_ARG       # misaligned
+    assert call(ks=2 * 128 + 4) == _lib.DMLA_ERR_INVALID_ARG         # k row stride not a multiple of 8
+    assert call(din=64) == _lib.DMLA_ERR_UNSUPPORTED
+    assert call(scale=0.0) == _lib.DMLA_ERR_INVALID_ARG
+    assert call(Sk=0) == _lib.DMLA_ERR_INVALID_ARG
+    assert call(Sq=1 << 25) == _lib.DMLA_ERR_UNSUPPORTED
+    assert call(B=0, ws_short=0) == _lib.DMLA_OK                     # empty: nothing launched
+    assert lib.dmla_last_error() == b""
+
+
+def test_onthefly_bwd_python_wrapper_rejects_cpu_tensors():
+    q = torch.zeros(1, 2, 4, 64, dtype=torch.bfloat16)
+    k = torch.zeros(1, 4, 2, 128, dtype=torch.bfloat16)
+    w = torch.zeros(2, 128, 64, dtype=torch.bfloat16)
+    m = torch.zeros(1, 2, 4)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.flash_dmla_bwd_onthefly(q, k, k, w, w, q, q, m, m)

@@ -91,6 +91,38 @@ def test_backward_matches_autograd_and_gradcheck():
                                         k[:1, :5].clone().requires_grad_(True)))
 
 
+def _otf_inputs(B, H, sq, sk, din, dl, seed):
+    q = seeded((B, H, sq, dl), seed, dtype=torch.float64)
+    k = seeded((B, sk, H, din), seed + 1, dtype=torch.float64)
+    v = seeded((B, sk, H, din), seed + 2, dtype=torch.float64)
+    wk = seeded((H, din, dl), seed + 3, 0.4, dtype=torch.float64)
+    wv = seeded((H, din, dl), seed + 4, 0.4, dtype=torch.float64)
+    do = seeded((B, H, sq, dl), seed + 5, dtype=torch.float64)
+    return q, k, v, wk, wv, do
+
+
+@pytest.mark.parametrize("sq,sk,causal", [(9, 13, True), (13, 9, True), (11, 11, False), (7, 16, False)])
+def test_onthefly_backward_matches_autograd(sq, sk, causal):
+    q, k, v, wk, wv, do = _otf_inputs(2, 3, sq, sk, 10, 6, 40 + sq)
+    o, m, l = R.dmla_fwd_onthefly(q, k, v, wk, wv, 0.4, causal, torch.float64)
+    got = R.dmla_bwd_onthefly(q, k, v, wk, wv, o, do, m, l, 0.4, causal, torch.float64)
+    ref = R.dmla_grads_onthefly_autograd(q, k, v, wk, wv, do, 0.4, causal)
+    for name, a, b in zip(("dq", "dk", "dv", "dwk", "dwv"), got, ref):
+        assert a.shape == b.shape, name
+        torch.testing.assert_close(a, b, atol=1e-12, rtol=1e-10, msg=name)
+    if causal and sq > sk:   # rows before the first key see nothing and get no gradient
+        assert torch.equal(got[0][:, :, :sq - sk], torch.zeros_like(got[0][:, :, :sq - sk]))
+
+
+def test_onthefly_backward_gradcheck():
+    q, k, v, wk, wv, _ = _otf_inputs(1, 2, 5, 6, 3, 4, 60)
+
+    def f(*xs):
+        return R.dmla_fwd_onthefly(*xs, 0.5, True, torch.float64)[0]
+
+    assert torch.autograd.gradcheck(f, tuple(t.clone().requires_grad_(True) for t in (q, k, v, wk, wv)))
+
+
 # ---------------------------------------------------------------- closed forms / invariants
 def test_causal_first_row_is_first_value():
     q = seeded((1, 2, 9, 16), 6, dtype=torch.float64)
@@ -205,6 +237,30 @@ def test_planted_backward_mistakes_are_caught(mistake):
     dq, dk = _mutant_bwd(q, k, o, do, m, l, 32, 1 / 8, mistake)
     bad = not (np.allclose(dq.numpy(), g["dq"], atol=1e-5) and np.allclose(dk.numpy(), g["dk_lat"], atol=1e-5))
     assert bad, f"golden gradients failed to catch the planted mistake {mistake}"
+
+
+def _mutant_otf_bwd(q, k, v, wk, wv, o, do, m, l, scale, mistake):
+    kl, vl = R.project_latent(k, wk), R.project_latent(v, wv)
+    s = R.masked_scores(q, kl, scale, True)
+    p = torch.exp(s - m.unsqueeze(-1)) / l.unsqueeze(-1)
+    ds = p * (do @ vl.transpose(-1, -2) - (do * o).sum(-1, keepdim=True))
+    dkl = (1.0 if mistake == "dk_lat_no_scale" else scale) * ds.transpose(-1, -2) @ q
+    dvl = p.transpose(-1, -2) @ do
+    dk = torch.einsum("bhsl,hdl->bshd", dkl, wv if mistake == "dk_through_wv" else wk)
+    dwk = torch.einsum("bshd,bhsl->hdl", k, dvl if mistake == "dwk_from_dv_lat" else dkl)
+    dwv = torch.einsum("bshd,bhsl->hdl", k if mistake == "dwv_from_k" else v, dvl)
+    return scale * ds @ kl, dk, torch.einsum("bhsl,hdl->bshd", dvl, wv), dwk, dwv
+
+
+@pytest.mark.parametrize("mistake", ["dk_lat_no_scale", "dk_through_wv", "dwk_from_dv_lat", "dwv_from_k"])
+def test_planted_onthefly_backward_mistakes_are_caught(mistake):
+    q, k, v, wk, wv, do = _otf_inputs(2, 2, 8, 8, 6, 6, 70)
+    o, m, l = R.dmla_fwd_onthefly(q, k, v, wk, wv, 0.4, True, torch.float64)
+    ref = R.dmla_grads_onthefly_autograd(q, k, v, wk, wv, do, 0.4, True)
+    got = _mutant_otf_bwd(q, k, v, wk, wv, o, do, m, l, 0.4, mistake)
+    same = all(torch.allclose(a, b, atol=1e-6) for a, b in zip(got, ref))
+    assert not same, f"autograd failed to catch the planted mistake {mistake}"
+    assert all(torch.allclose(a, b, atol=1e-10) for a, b in zip(_mutant_otf_bwd(q, k, v, wk, wv, o, do, m, l, 0.4, "none"), ref))
 
 
 @pytest.mark.parametrize("mistake", ["v_wrong_slice", "k_transposed_dims", "unscaled_m", "mask_off_by_one"])

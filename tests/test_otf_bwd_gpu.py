@@ -1,0 +1,160 @@
+"""Parity of the on-the-fly backward (dmla_bwd_onthefly) with fp32 references.
+
+Each case runs this library's on-the-fly forward, then its backward from the saved (o, m, l),
+and checks dq, dk, dv, dwk and dwv twice:
+  * against the closed-form oracle backward fed with the same o, m, l -- isolates the
+    backward kernels;
+  * against fp32 torch.autograd through the exact on-the-fly forward -- the end-to-end
+    gradient of the op.
+The first comparison is held to the north-star tolerance (max-abs 2e-2, mean-rel 1e-2).  The
+second cannot be, for any kernel: D = rowsum(dO * O) takes the forward's bf16 O, and that
+rounding alone moves dwk by up to ~3e-2 at these sizes (the exact math fed with the
+bf16-rounded O, in fp64, against the exact gradient).  So against autograd each gradient may
+differ by that same-O error of the oracle plus 2e-2 max-abs, and by 1e-2 mean-rel.  dwk and dwv
+are compared in fp32, the op's default output type: they sum over every batch element and
+position and reach ~30 at config-4 sizes, where a bf16 rounding alone is 0.06.  Inputs follow BASELINE config 4:
+q, k, v ~ N(0, 1), Xavier-uniform weights, scale 1/8, dO ~ N(0, 1).
+"""
+import math
+
+import pytest
+import torch
+
+from conftest import OUT_MAX_ABS, OUT_MEAN_REL, assert_out_close, seeded
+from oracle import dmla_ref as R
+from python import ops
+
+NAMES = ("dq", "dk", "dv", "dwk", "dwv")
+
+
+def _inputs(B, H, Sq, Sk, seed):
+    q = seeded((B, H, Sq, 64), seed, 1.0, torch.bfloat16)
+    k = seeded((B, Sk, H, 128), seed + 1, 1.0, torch.bfloat16)
+    v = seeded((B, Sk, H, 128), seed + 2, 1.0, torch.bfloat16)
+    bound = math.sqrt(6.0 / (128 + 64))
+    g = torch.Generator().manual_seed(seed + 3)
+    wk = ((torch.rand(H, 128, 64, generator=g) * 2 - 1) * bound).to(torch.bfloat16)
+    wv = ((torch.rand(H, 128, 64, generator=g) * 2 - 1) * bound).to(torch.bfloat16)
+    do = seeded((B, H, Sq, 64), seed + 4, 1.0, torch.bfloat16)
+    return q, k, v, wk, wv, do
+
+
+def _run(gpu, xs, causal, scale=0.125, **kw):
+    q, k, v, wk, wv, do = (t.to(gpu) for t in xs)
+    o, m, l = ops.flash_dmla_fwd_onthefly(q, k, v, wk, wv, scale, causal, return_stats=True)
+    grads = ops.flash_dmla_bwd_onthefly(q, k, v, wk, wv, o, do, m, l, scale, causal, **kw)
+    torch.cuda.synchronize()
+    return o, m, l, grads
+
+
+def _check(gpu, B, H, Sq, Sk, causal, seed, ref_device="cpu", autograd=True, scale=0.125):
+    xs = _inputs(B, H, Sq, Sk, seed)
+    o, m, l, grads = _run(gpu, xs, causal, scale)
+    assert [g.dtype for g in grads] == [torch.bfloat16] * 3 + [torch.float32] * 2
+    dev = gpu if ref_device == "gpu" else torch.device("cpu")
+    q, k, v, wk, wv, do = (t.to(dev).float() for t in xs)
+    ref = R.dmla_bwd_onthefly(q, k, v, wk, wv, o.to(dev).float(), do, m.to(dev), l.to(dev), scale, causal)
+    for name, g, r in zip(NAMES, grads, ref):
+        assert tuple(g.shape) == tuple(r.shape), name
+        assert_out_close(g, r, f"{name} vs oracle backward")
+    if autograd:
+        ag = R.dmla_grads_onthefly_autograd(q, k, v, wk, wv, do, scale, causal, torch.float32)
+        for name, g, r, a in zip(NAMES, grads, ref, ag):
+            a = a.to(g.device)
+            same_o = (r.to(g.device) - a).abs().max().item()   # the bf16 O's share, no kernel involved
+            diff = (g.float() - a).abs()
+            assert diff.max().item() <= same_o + OUT_MAX_ABS, \
+                f"{name} vs fp32 autograd: max-abs {diff.max().item():.3e} > {same_o:.3e} + {OUT_MAX_ABS}"
+            mean_rel = (diff.mean() / a.abs().mean().clamp_min(1e-30)).item()
+            assert mean_rel <= OUT_MEAN_REL, f"{name} vs fp32 autograd: mean-rel {mean_rel:.3e}"
+    return grads
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize(
+    "B,H,Sq,Sk,causal",
+    [
+        (1, 2, 64, 64, True),       # one key block, one row block
+        (2, 3, 200, 200, True),     # ragged rows and keys, padded blocks
+        (1, 2, 77, 130, True),      # Sq < Sk: bottom-right aligned causal
+        (1, 2, 150, 70, True),      # Sq > Sk: the first rows see no key and get no gradient
+        (2, 2, 96, 96, False),      # non-causal
+        (1, 2, 100, 1100, False),   # two 1024-key weight-gradient chunks
+        (1, 1, 1030, 1030, True),   # causal across the chunk boundary
+        (1, 3, 5, 5, True),         # a handful of tokens
+    ],
+)
+def test_otf_bwd_small_shapes(gpu, B, H, Sq, Sk, causal):
+    grads = _check(gpu, B, H, Sq, Sk, causal, seed=B * 100 + H * 10 + Sq)
+    if causal and Sq > Sk:
+        assert torch.equal(grads[0][:, :, :Sq - Sk].float().cpu(), torch.zeros(B, H, Sq - Sk, 64))
+
+
+@pytest.mark.gpu
+def test_otf_bwd_single_token(gpu):
+    """One key: softmax is constant, so the exact dq, dk and dwk are 0 and dS = dP - D is pure
+    rounding (fp16 V_lat against the bf16 O); they must stay small, while dv = dO and
+    dwv = v^T dO are checked at the bar."""
+    xs = _inputs(1, 2, 1, 1, 5)
+    _, _, _, grads = _run(gpu, xs, True)
+    q, k, v, wk, wv, do = (t.float() for t in xs)
+    ag = R.dmla_grads_onthefly_autograd(q, k, v, wk, wv, do, 0.125, True, torch.float32)
+    for name, g, a in zip(NAMES, grads, ag):
+        if name in ("dq", "dk", "dwk"):
+            assert a.abs().max().item() == 0.0
+            assert g.float().abs().max().item() <= OUT_MAX_ABS, name
+        else:
+            assert_out_close(g, a, name)
+
+
+@pytest.mark.gpu
+def test_otf_bwd_config4_shape(gpu):
+    """BASELINE config 4 at full size (B=2, H=32, S=4096), oracle on the GPU in fp32."""
+    _check(gpu, 2, 32, 4096, 4096, True, seed=4, ref_device="gpu", autograd=False)
+
+
+@pytest.mark.gpu
+def test_otf_bwd_config4_autograd_heads(gpu):
+    """Full sequence length on 4 heads against fp32 autograd on the GPU."""
+    _check(gpu, 2, 4, 4096, 4096, True, seed=44, ref_device="gpu")
+
+
+@pytest.mark.gpu
+def test_otf_bwd_deterministic_and_bf16_weights(gpu):
+    xs = _inputs(1, 4, 300, 300, 7)
+    _, _, _, g1 = _run(gpu, xs, True)
+    _, _, _, g2 = _run(gpu, xs, True)
+    for name, a, b in zip(NAMES, g1, g2):
+        assert torch.equal(a, b), f"{name} differs between identical calls"
+    _, _, _, g3 = _run(gpu, xs, True, dw_dtype=torch.bfloat16)
+    for name, a, b in zip(NAMES, g1, g3):
+        assert b.dtype == torch.bfloat16
+        assert torch.equal(a.to(torch.bfloat16), b), f"{name}: bf16 output is not the rounded fp32 one"
+
+
+@pytest.mark.gpu
+def test_otf_autograd_function(gpu):
+    xs = _inputs(1, 2, 140, 140, 11)
+    leaves = [t.to(gpu).requires_grad_(True) for t in xs[:5]]
+    o = ops.flash_dmla_onthefly(*leaves, 0.125, True)
+    o.backward(xs[5].to(gpu))
+    _, _, _, grads = _run(gpu, xs, True)
+    for name, leaf, g in zip(NAMES, leaves, grads):
+        assert leaf.grad is not None and leaf.grad.dtype == torch.bfloat16, name
+        assert torch.equal(leaf.grad, g.to(torch.bfloat16)), f"{name}: autograd differs from the direct call"
+
+
+@pytest.mark.gpu
+def test_otf_bwd_strided_inputs(gpu):
+    """Non-contiguous views: k, v inside a wider [B, Sk, H, 2*128] buffer, q/o/do head-major views."""
+    B, H, Sq, Sk = 1, 2, 96, 96
+    q, k, v, wk, wv, do = _inputs(B, H, Sq, Sk, 13)
+    kv = torch.cat([k, v], dim=-1).to(gpu)
+    kg, vg = kv[..., :128], kv[..., 128:]
+    qg = q.transpose(1, 2).contiguous().to(gpu).transpose(1, 2)      # [B, H, Sq, 64] with seq-major storage
+    dog = do.transpose(1, 2).contiguous().to(gpu).transpose(1, 2)
+    o, m, l = ops.flash_dmla_fwd_onthefly(qg, kg, vg, wk.to(gpu), wv.to(gpu), 0.125, True, return_stats=True)
+    grads = ops.flash_dmla_bwd_onthefly(qg, kg, vg, wk.to(gpu), wv.to(gpu), o, dog, m, l, 0.125, True)
+    _, _, _, ref = _run(gpu, (q, k, v, wk, wv, do), True)
+    for name, a, b in zip(NAMES, grads, ref):
+        assert torch.equal(a, b), f"{name}: strided inputs change the result"
