@@ -16,7 +16,9 @@ counting B*H*S(S+1)*(576+512) flops (unmasked causal pairs only).
 `secondary` carries the paged decode (config 3) in KV GB/s with its own HBM roofline, timed
 the same way with rotating KV pools larger than the 256 MB MALL, the cache-latent backward
 (config 5) in TFLOP/s, counting B*H*S(S+1)*(3*576+2*512) flops, and the on-the-fly forward
-(config 4) in TFLOP/s, counting B*H*S(S+1)*128 + 4*B*S*H*128*64 flops (projection once).
+(config 4) in TFLOP/s, counting B*H*S(S+1)*128 + 4*B*S*H*128*64 flops (projection once),
+and the on-the-fly backward at the config-4 shapes, counting B*H*S(S+1)*320 + 8*B*S*H*128*64
+flops (five products per causal pair plus the four projection gradients).
 """
 import argparse
 import json
@@ -321,6 +323,69 @@ def cpu_bwd(q, k, o, do, m, l, flops, budget_s):
             "seconds": t}
 
 
+def bench_onthefly_bwd(steps, warmup, cpu_baseline):
+    """On-the-fly backward (all six kernels) at the config-4 shapes from one forward's o, m, l."""
+    import torch
+
+    from python import ops
+
+    B, H, S = 2, 32, 4096
+    dev = torch.device("cuda:0")
+    q = _seeded((B, H, S, 64), 10, 1.0, torch.bfloat16).to(dev)
+    k = _seeded((B, S, H, 128), 11, 1.0, torch.bfloat16).to(dev)
+    v = _seeded((B, S, H, 128), 12, 1.0, torch.bfloat16).to(dev)
+    do = _seeded((B, H, S, 64), 14, 1.0, torch.bfloat16).to(dev)
+    bound = math.sqrt(6.0 / (128 + 64))
+    g = torch.Generator().manual_seed(13)
+    wk = ((torch.rand(H, 128, 64, generator=g) * 2 - 1) * bound).to(torch.bfloat16).to(dev)
+    wv = ((torch.rand(H, 128, 64, generator=g) * 2 - 1) * bound).to(torch.bfloat16).to(dev)
+    o, m, l = ops.flash_dmla_fwd_onthefly(q, k, v, wk, wv, 0.125, True, return_stats=True)
+    # Five products per unmasked (row, key) pair (S, dP, dV_lat, dK_lat, dQ: 2 * 64 flops each)
+    # plus the projection gradients dK, dV, dWK, dWV (2 * B*S*H*128*64 each); the recomputed
+    # K_lat / V_lat are not credited.
+    flops = B * H * S * (S + 1) * 5 * 64 + 4 * (2 * B * S * H * 128 * 64)
+
+    def step(i=0):
+        ops.flash_dmla_bwd_onthefly(q, k, v, wk, wv, o, do, m, l, 0.125, True)
+
+    wall_ms, kern_ms = _time_launches(step, steps, warmup)
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    res = {
+        "metric": "DMLA on-the-fly backward TFLOP/s (config-4 shapes)",
+        "value": flops / (wall_ms * 1e-3) / 1e12,
+        "unit": "TFLOP/s",
+        "ms_per_step": wall_ms,
+        "config": {"workload": "on-the-fly backward at the BASELINE config 4 shapes", "batch": B, "heads": H,
+                   "seq_len": S, "d_in": 128, "d_lat": 64, "causal": True, "softmax_scale": 0.125},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": _load_traffic("onthefly_bwd"),
+                     "kernel": "otf_bwd_prep + proj + dkdv + dq + wgrad + wreduce", "kernel_ms": kern_ms,
+                     "algorithmic_flops_per_launch": flops},
+    }
+    if cpu_baseline:
+        res["cpu_baseline"] = cpu_onthefly_bwd([t.cpu() for t in (q, k, v, wk, wv, o, do, m, l)], flops,
+                                               cpu_baseline)
+    return res
+
+
+def cpu_onthefly_bwd(ts, flops, budget_s):
+    """fp32 eager closed-form oracle backward on batch element 0, repeated for ~budget_s s."""
+    import torch
+
+    from oracle import dmla_ref as R
+
+    torch.set_num_threads(_cpu_threads())
+    q, k, v, wk, wv, o, do, m, l = ts
+    B = q.shape[0]
+    xs = [q[:1].float(), k[:1].float(), v[:1].float(), wk.float(), wv.float(), o[:1].float(), do[:1].float(),
+          m[:1], l[:1]]
+    n, t = _time_repeated(lambda: R.dmla_bwd_onthefly(*xs, 0.125, True), budget_s)
+    return {"value": n * flops / B / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"batch element 0 of the config-4 shapes through the fp32 eager oracle backward, "
+                      f"{n} passes in {t:.1f} s",
+            "seconds": t}
+
+
 def copy_calibration(mib):
     """Streaming copies of `mib` MiB for calibrating the HBM byte counters.  torch's elementwise
     negation kernel is a plain copy (it reads N bytes and writes N bytes), so FETCH_SIZE and
@@ -341,8 +406,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=30)
-    ap.add_argument("--secondary", default="decode,bwd,onthefly",
-                    help="comma list of extra workloads: decode, bwd, onthefly")
+    ap.add_argument("--secondary", default="decode,bwd,onthefly,onthefly_bwd",
+                    help="comma list of extra workloads: decode, bwd, onthefly, onthefly_bwd")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget per workload")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -371,6 +436,8 @@ def main():
             secondary["bwd"] = bench_bwd(args.steps, args.warmup, cpu)
         elif name == "onthefly":
             secondary["onthefly"] = bench_onthefly(args.steps, args.warmup, cpu)
+        elif name == "onthefly_bwd":
+            secondary["onthefly_bwd"] = bench_onthefly_bwd(args.steps, args.warmup, cpu)
         else:
             raise SystemExit(f"unknown secondary workload {name}")
     line = {

@@ -9,9 +9,10 @@
 //     dK = dK_lat WK^T,  dWK[h] = sum_{b,s} K[b,s,h,:]^T dK_lat[b,h,s,:]   (same for V / WV).
 // The reference has no on-the-fly backward at all (WK / WV are learnable per README.md:14).
 //
-// Six kernels run in order on one stream, all deterministic (no atomics):
+// Seven kernels run in order on one stream, all deterministic (no atomics):
 //   otf_bwd_prep_kernel    per query row: Q and dO as fp16, lse2 = (m + ln l) log2(e), D;
-//   otf_bwd_proj_kernel    K_lat and V_lat as fp16 (the forward's projection, same MFMA order);
+//   otf_bwd_wt_kernel      WK^T and WV^T;
+//   otf_bwd_proj_kernel    K_lat and V_lat as fp16 (the forward's projection, same values);
 //   otf_bwd_dkdv_kernel    per 128 keys: dK_lat, dV_lat over the rows that see them;
 //   otf_bwd_dq_kernel      per 128 rows: dQ over the keys they see (S and dP recomputed);
 //   otf_bwd_wgrad_kernel   per (tensor, head, 1024 keys): dK / dV and a dWK / dWV partial;
@@ -25,6 +26,8 @@
 // the B operand of a product contracting over those 32 rows when the k-index runs over rows
 // {4g+i} then {16+4g+i} (g = l/16); ds_read_b64_tr_b16 on a row-major tile hands the A operand
 // exactly that row order (two reads, rows 4g.. and 16+4g..).  So P and dS never go through LDS.
+#include <type_traits>
+
 #include "dmla_common.h"
 #include "dmla_host.h"
 
@@ -72,6 +75,7 @@ struct OtfBwdParams {
   _Float16* dklat;       // [B*H][Skp][64]; padding keys zero
   _Float16* dvlat;
   float* wpart;          // [2][H][B*n_sc][128][64] fp32 partial weight gradients
+  bf16* wt;              // [2][H][64][128]: WK^T, WV^T
 };
 
 __device__ __forceinline__ f16x8 to_f16(const bf16x8& x) {
@@ -138,66 +142,66 @@ __global__ void __launch_bounds__(256) otf_bwd_prep_kernel(OtfBwdParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Projection with the forward's operands and k-step order, rounded to fp16 as there:
-// K_lat^T = WK^T K^T (A = WK^T rows, B = raw K rows) and V_lat = V WV (A = raw V rows, B = WV^T
-// rows), four k-steps of 32 input dims each.  Block = 256 keys of one (b, h); wave w takes the
-// 16-key blocks w, w+4, ...; grid (Skp / 256 rounded up, H, B).
+// W^T of both projections into the workspace: wt[x][h][dim][in], x = 0 for WK, 1 for WV.
+// Grid (H, 2); thread t reads input dim t/2, latent dims 32 (t%2) .. +31.
+__global__ void __launch_bounds__(256) otf_bwd_wt_kernel(OtfBwdParams p) {
+  const int h = blockIdx.x, x = blockIdx.y;
+  const bf16* w = (x ? p.wv : p.wk) + h * p.w_sh + (threadIdx.x >> 1) * p.w_si + 32 * (threadIdx.x & 1);
+  bf16* wt = p.wt + ((size_t)x * p.H + h) * (kLat * kIn) + (threadIdx.x >> 1);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const bf16x8 a = *reinterpret_cast<const bf16x8*>(w + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wt[(32 * (threadIdx.x & 1) + 8 * c + e) * kIn] = a[e];
+  }
+}
+
+// Projection as the forward computes it, rounded to fp16 as there: X_lat^T = W^T X^T with
+// A = W^T rows and B = raw X rows (K: the forward's own operand order; V: the forward's
+// V_lat = V WV with A and B swapped, which v_mfma_f32_16x16x32_bf16 computes bit for bit as
+// the transpose), four k-steps of 32 input dims each.  Block = 256 keys of one (b, h); waves
+// 0-1 project K, waves 2-3 V, each taking every other 16-key block with the next block's rows
+// loaded while the current one is multiplied.  Grid (Skp / 256 rounded up, H, B).
 __global__ void __launch_bounds__(256) otf_bwd_proj_kernel(OtfBwdParams p) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * kLat * kIn * 2];   // WK^T, WV^T: [dim][in]
-  DMLA_LDS char* lds = (DMLA_LDS char*)smem;
   const int h = blockIdx.y, b = blockIdx.z, bh = b * p.H + h;
   const int wave = uniform(threadIdx.x >> 6), lane = lane_id(), l16 = lane & 15, g = lane >> 4;
-  // W^T rows of 256 B, chunk c of row r at c ^ (r & 15).
-  for (int idx = threadIdx.x; idx < kIn * kLat / 8; idx += 256) {
-    const int i = idx / (kLat / 8), j8 = idx % (kLat / 8);
-    const bf16x8 a = *reinterpret_cast<const bf16x8*>(p.wk + h * p.w_sh + i * p.w_si + 8 * j8);
-    const bf16x8 c = *reinterpret_cast<const bf16x8*>(p.wv + h * p.w_sh + i * p.w_si + 8 * j8);
+  const int x = wave >> 1;
+  bf16x8 wa[4][4];   // [db][ks]: W^T row 16 db + l16, input dims 32 ks + 8 g ..
+  {
+    const bf16* wt = p.wt + ((size_t)x * p.H + h) * (kLat * kIn) + l16 * kIn + 8 * g;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int j = 8 * j8 + e;
-      const int o = j * 256 + 16 * ((i >> 3) ^ (j & 15)) + 2 * (i & 7);
-      *reinterpret_cast<DMLA_LDS bf16*>(lds + o) = a[e];
-      *reinterpret_cast<DMLA_LDS bf16*>(lds + kLat * kIn * 2 + o) = c[e];
-    }
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) wa[db][ks] = *reinterpret_cast<const bf16x8*>(wt + 16 * db * kIn + 32 * ks);
   }
-  __syncthreads();
-  bf16x8 wka[4][4], wvb[4][4];   // [db][ks]: W^T row 16 db + l16, input dims 32 ks + 8 g ..
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int r = 16 * db + l16, o = r * 256 + 16 * ((4 * ks + g) ^ (r & 15));
-      wka[db][ks] = *reinterpret_cast<const DMLA_LDS bf16x8*>(lds + o);
-      wvb[db][ks] = *reinterpret_cast<const DMLA_LDS bf16x8*>(lds + kLat * kIn * 2 + o);
-    }
+  const bf16* src = x ? p.v + b * p.v_sb + h * p.v_sh : p.k + b * p.k_sb + h * p.k_sh;
+  const int64_t ss = x ? p.v_ss : p.k_ss;
+  _Float16* dst = (x ? p.vlat : p.klat) + (size_t)bh * p.Skp * kLat;
   const int key_base = blockIdx.x * 256;
-  for (int kb = wave; kb < 16 && key_base + 16 * kb < p.Skp; kb += 4) {
-    const int key = key_base + 16 * kb + l16;
-    const int gk = min(key, p.Sk - 1);
-    bf16x8 kx[4], vx[4];
+  const int n_kb = min(16, (p.Skp - key_base) / 16);
+  bf16x8 xr[4];
+  auto load = [&](int kb) {
+    const int gk = min(key_base + 16 * kb + l16, p.Sk - 1);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      kx[ks] = *reinterpret_cast<const bf16x8*>(p.k + b * p.k_sb + (int64_t)gk * p.k_ss + h * p.k_sh + 32 * ks + 8 * g);
-      vx[ks] = *reinterpret_cast<const bf16x8*>(p.v + b * p.v_sb + (int64_t)gk * p.v_ss + h * p.v_sh + 32 * ks + 8 * g);
-    }
-    const size_t row = ((size_t)bh * p.Skp + key) * kLat;
-    const int key4 = key_base + 16 * kb + 4 * g;   // V_lat rows of this lane: key4 + i
+    for (int ks = 0; ks < 4; ++ks) xr[ks] = *reinterpret_cast<const bf16x8*>(src + (int64_t)gk * ss + 32 * ks + 8 * g);
+  };
+  int kb = wave & 1;
+  if (kb < n_kb) load(kb);
+  for (; kb < n_kb; kb += 2) {
+    bf16x8 cur[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) cur[ks] = xr[ks];
+    if (kb + 2 < n_kb) load(kb + 2);
+    const int key = key_base + 16 * kb + l16;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      f32x4 ck = {0.f, 0.f, 0.f, 0.f}, cv = {0.f, 0.f, 0.f, 0.f};
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        ck = mfma_bf16(wka[db][ks], kx[ks], ck);   // K_lat^T[dim 16 db + 4 g + i][key]
-        cv = mfma_bf16(vx[ks], wvb[db][ks], cv);   // V_lat[key4 + i][dim 16 db + l16]
-      }
-      f16x4 a;
+      for (int ks = 0; ks < 4; ++ks) c = mfma_bf16(wa[db][ks], cur[ks], c);   // X_lat^T[dim 16 db + 4 g + i][key]
+      f16x4 o;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[i] = key < p.Sk ? (_Float16)ck[i] : (_Float16)0.f;
-        p.vlat[((size_t)bh * p.Skp + key4 + i) * kLat + 16 * db + l16] =
-            key4 + i < p.Sk ? (_Float16)cv[i] : (_Float16)0.f;
-      }
-      *reinterpret_cast<f16x4*>(p.klat + row + 16 * db + 4 * g) = a;
+      for (int i = 0; i < 4; ++i) o[i] = key < p.Sk ? (_Float16)c[i] : (_Float16)0.f;
+      *reinterpret_cast<f16x4*>(dst + (size_t)key * kLat + 16 * db + 4 * g) = o;
     }
   }
 }
@@ -247,66 +251,82 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
   const unsigned lbase = lds_addr(lds);
   const float sl2 = p.scale_log2;
 
+  // One 32-row sub-tile; kMask applies the causal / key-range mask (only sub-tiles that reach
+  // past some pair's limit need it), so the common case is straight-line code.
+  auto subtile = [&](const DMLA_LDS char* qt, const DMLA_LDS char* dt, int r0, const float4 (&e)[4], auto mask_tag) {
+    constexpr bool kMask = decltype(mask_tag)::value;
+    f32x4 sacc[2][2], dpacc[2][2];   // [rb][kb]: rows 16 rb + 4 g + i, key 16 kb + l16
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const f16x8 qa0 = lds_f16x8(qt + row_operand_off(lane, rb, 0));
+      const f16x8 qa1 = lds_f16x8(qt + row_operand_off(lane, rb, 1));
+      const f16x8 oa0 = lds_f16x8(dt + row_operand_off(lane, rb, 0));
+      const f16x8 oa1 = lds_f16x8(dt + row_operand_off(lane, rb, 1));
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        sacc[rb][kb] = mfma_f16(qa0, kreg[kb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+        sacc[rb][kb] = mfma_f16(qa1, kreg[kb][1], sacc[rb][kb]);
+        dpacc[rb][kb] = mfma_f16(oa0, vreg[kb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+        dpacc[rb][kb] = mfma_f16(oa1, vreg[kb][1], dpacc[rb][kb]);
+      }
+    }
+    f16x8 pb[2], dsb[2];   // [kb]: B operands, slot 4 rb + i = row 16 rb + 4 g + i
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const float4 ea = e[2 * rb], eb = e[2 * rb + 1];
+      const float lse[4] = {ea.x, ea.z, eb.x, eb.z};
+      const float dd[4] = {ea.y, ea.w, eb.y, eb.w};
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float pv = fast_exp2(__builtin_fmaf(sacc[rb][kb][i], sl2, -lse[i]));
+          if constexpr (kMask) {
+            const int row = r0 + 16 * rb + 4 * g + i, key = k0 + 16 * kb + l16;
+            const int lim = p.causal ? min(row + off, p.Sk - 1) : p.Sk - 1;
+            pv = key > lim ? 0.f : pv;
+          }
+          pb[kb][4 * rb + i] = (_Float16)pv;
+          dsb[kb][4 * rb + i] = (_Float16)(pv * (dpacc[rb][kb][i] - dd[i]));
+        }
+    }
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const f16x8 ot = lds_col_operand(dt, lane, db);   // dO^T[dim 16 db + l16][rows]
+      const f16x8 qtt = lds_col_operand(qt, lane, db);  // Q^T
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        dvt[db][kb] = mfma_f16(ot, pb[kb], dvt[db][kb]);
+        dkt[db][kb] = mfma_f16(qtt, dsb[kb], dkt[db][kb]);
+      }
+    }
+  };
+
   if (n_st > 0) stage_pair(qsrc, dsrc, rs0, lbase, wave, lane);
   for (int s = 0; s < n_st; ++s) {
     wait_vmem();
     __syncthreads();   // stage s complete; every wave is done with stage s-1
+    // (lse2, D) of rows r0 + 16 rb + 4 g + i, four float2 = two float4 per row block; loaded
+    // before the next stage's copies so that waiting for them does not wait for the copies.
+    float4 e[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const float4* lp = reinterpret_cast<const float4*>(lsed + rs0 + 64 * s + 32 * t + 4 * g);
+      e[t][0] = lp[0];
+      e[t][1] = lp[1];
+      e[t][2] = lp[8];
+      e[t][3] = lp[9];
+    }
     if (s + 1 < n_st) stage_pair(qsrc, dsrc, rs0 + 64 * (s + 1), lbase + ((s + 1) & 1) * kStage, wave, lane);
     const DMLA_LDS char* st = lds + (s & 1) * kStage;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int r0 = rs0 + 64 * s + 32 * t;
       if (r0 >= p.Sq || (p.causal && k0 > r0 + 31 + off)) continue;   // padding only / all masked
-      const DMLA_LDS char* qt = st + t * kTile;
-      const DMLA_LDS char* dt = st + (2 + t) * kTile;
-      // (lse2, D) of rows r0 + 16 rb + 4 g + i: 4 float2 = two float4 per row block
-      const float4* lp = reinterpret_cast<const float4*>(lsed + r0 + 4 * g);
-      const float4 e00 = lp[0], e01 = lp[1], e10 = lp[8], e11 = lp[9];
-      f32x4 sacc[2][2], dpacc[2][2];   // [rb][kb]: rows 16 rb + 4 g + i, key 16 kb + l16
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        const f16x8 qa0 = lds_f16x8(qt + row_operand_off(lane, rb, 0));
-        const f16x8 qa1 = lds_f16x8(qt + row_operand_off(lane, rb, 1));
-        const f16x8 oa0 = lds_f16x8(dt + row_operand_off(lane, rb, 0));
-        const f16x8 oa1 = lds_f16x8(dt + row_operand_off(lane, rb, 1));
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          sacc[rb][kb] = mfma_f16(qa0, kreg[kb][0], f32x4{0.f, 0.f, 0.f, 0.f});
-          sacc[rb][kb] = mfma_f16(qa1, kreg[kb][1], sacc[rb][kb]);
-          dpacc[rb][kb] = mfma_f16(oa0, vreg[kb][0], f32x4{0.f, 0.f, 0.f, 0.f});
-          dpacc[rb][kb] = mfma_f16(oa1, vreg[kb][1], dpacc[rb][kb]);
-        }
-      }
-      const bool need_mask = k0 + 31 >= p.Sk || (p.causal && k0 + 31 > r0 + off);
-      f16x8 pb[2], dsb[2];   // [kb]: B operands, slot 4 rb + i = row 16 rb + 4 g + i
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        const float4 ea = rb ? e10 : e00, eb = rb ? e11 : e01;
-        const float lse[4] = {ea.x, ea.z, eb.x, eb.z};
-        const float dd[4] = {ea.y, ea.w, eb.y, eb.w};
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float pv = fast_exp2(__builtin_fmaf(sacc[rb][kb][i], sl2, -lse[i]));
-            if (need_mask) {
-              const int row = r0 + 16 * rb + 4 * g + i, key = k0 + 16 * kb + l16;
-              if (key >= p.Sk || (p.causal && key > row + off)) pv = 0.f;
-            }
-            pb[kb][4 * rb + i] = (_Float16)pv;
-            dsb[kb][4 * rb + i] = (_Float16)(pv * (dpacc[rb][kb][i] - dd[i]));
-          }
-      }
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const f16x8 ot = lds_col_operand(dt, lane, db);   // dO^T[dim 16 db + l16][rows]
-        const f16x8 qtt = lds_col_operand(qt, lane, db);  // Q^T
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          dvt[db][kb] = mfma_f16(ot, pb[kb], dvt[db][kb]);
-          dkt[db][kb] = mfma_f16(qtt, dsb[kb], dkt[db][kb]);
-        }
-      }
+      if (k0 + 31 >= p.Sk || (p.causal && k0 + 31 > r0 + off))
+        subtile(st + t * kTile, st + (2 + t) * kTile, r0, e[t], std::true_type{});
+      else
+        subtile(st + t * kTile, st + (2 + t) * kTile, r0, e[t], std::false_type{});
     }
   }
   // dK_lat = scale dS^T Q and dV_lat = P^T dO as fp16 rows (keys past Sk hold zeros: P = 0 there)
@@ -373,6 +393,46 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
   const unsigned lbase = lds_addr(lds);
   const float sl2 = p.scale_log2;
 
+  auto subtile = [&](const DMLA_LDS char* kt, const DMLA_LDS char* vt, int c0, auto mask_tag) {
+    constexpr bool kMask = decltype(mask_tag)::value;
+    f32x4 sT[2][2], dpT[2][2];   // [kb][rb]: keys 16 kb + 4 g + i, row 16 rb + l16
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const f16x8 ka0 = lds_f16x8(kt + row_operand_off(lane, kb, 0));
+      const f16x8 ka1 = lds_f16x8(kt + row_operand_off(lane, kb, 1));
+      const f16x8 va0 = lds_f16x8(vt + row_operand_off(lane, kb, 0));
+      const f16x8 va1 = lds_f16x8(vt + row_operand_off(lane, kb, 1));
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        sT[kb][rb] = mfma_f16(ka0, qreg[rb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+        sT[kb][rb] = mfma_f16(ka1, qreg[rb][1], sT[kb][rb]);
+        dpT[kb][rb] = mfma_f16(va0, oreg[rb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+        dpT[kb][rb] = mfma_f16(va1, oreg[rb][1], dpT[kb][rb]);
+      }
+    }
+    f16x8 dsa[2];   // [rb]: A operand, slot 4 kb + i = key 16 kb + 4 g + i
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float pv = fast_exp2(__builtin_fmaf(sT[kb][rb][i], sl2, -lse[rb]));
+          if constexpr (kMask) {
+            const int row = r0 + 16 * rb + l16, key = c0 + 16 * kb + 4 * g + i;
+            const int lim = p.causal ? min(row + off, p.Sk - 1) : p.Sk - 1;
+            pv = key > lim ? 0.f : pv;
+          }
+          dsa[rb][4 * kb + i] = (_Float16)(pv * (dpT[kb][rb][i] - dd[rb]));
+        }
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const f16x8 kb_t = lds_col_operand(kt, lane, db);   // K_lat[keys][dim 16 db + l16]
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) dq[rb][db] = mfma_f16(dsa[rb], kb_t, dq[rb][db]);
+    }
+  };
+
   if (n_st > 0) stage_pair(ksrc, vsrc, 0, lbase, wave, lane);
   for (int s = 0; s < n_st; ++s) {
     wait_vmem();
@@ -383,44 +443,10 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
     for (int t = 0; t < 2; ++t) {
       const int c0 = 64 * s + 32 * t;
       if (c0 >= key_end || (p.causal && c0 > r0 + 31 + off)) continue;
-      const DMLA_LDS char* kt = st + t * kTile;
-      const DMLA_LDS char* vt = st + (2 + t) * kTile;
-      f32x4 sT[2][2], dpT[2][2];   // [kb][rb]: keys 16 kb + 4 g + i, row 16 rb + l16
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const f16x8 ka0 = lds_f16x8(kt + row_operand_off(lane, kb, 0));
-        const f16x8 ka1 = lds_f16x8(kt + row_operand_off(lane, kb, 1));
-        const f16x8 va0 = lds_f16x8(vt + row_operand_off(lane, kb, 0));
-        const f16x8 va1 = lds_f16x8(vt + row_operand_off(lane, kb, 1));
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-          sT[kb][rb] = mfma_f16(ka0, qreg[rb][0], f32x4{0.f, 0.f, 0.f, 0.f});
-          sT[kb][rb] = mfma_f16(ka1, qreg[rb][1], sT[kb][rb]);
-          dpT[kb][rb] = mfma_f16(va0, oreg[rb][0], f32x4{0.f, 0.f, 0.f, 0.f});
-          dpT[kb][rb] = mfma_f16(va1, oreg[rb][1], dpT[kb][rb]);
-        }
-      }
-      const bool need_mask = c0 + 31 >= p.Sk || (p.causal && c0 + 31 > r0 + off);
-      f16x8 dsa[2];   // [rb]: A operand, slot 4 kb + i = key 16 kb + 4 g + i
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float pv = fast_exp2(__builtin_fmaf(sT[kb][rb][i], sl2, -lse[rb]));
-            if (need_mask) {
-              const int row = r0 + 16 * rb + l16, key = c0 + 16 * kb + 4 * g + i;
-              if (key >= p.Sk || (p.causal && key > row + off)) pv = 0.f;
-            }
-            dsa[rb][4 * kb + i] = (_Float16)(pv * (dpT[kb][rb][i] - dd[rb]));
-          }
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const f16x8 kb_t = lds_col_operand(kt, lane, db);   // K_lat[keys][dim 16 db + l16]
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) dq[rb][db] = mfma_f16(dsa[rb], kb_t, dq[rb][db]);
-      }
+      if (c0 + 31 >= p.Sk || (p.causal && c0 + 31 > r0 + off))
+        subtile(st + t * kTile, st + (2 + t) * kTile, c0, std::true_type{});
+      else
+        subtile(st + t * kTile, st + (2 + t) * kTile, c0, std::false_type{});
     }
   }
 #pragma unroll
@@ -558,24 +584,23 @@ __global__ void __launch_bounds__(256) otf_bwd_wgrad_kernel(OtfBwdParams p) {
       for (int i = 0; i < 4; ++i) part[(16 * (2 * wave + a) + 4 * g + i) * kLat + 16 * db + l16] = dw[a][db][i];
 }
 
-// dW[h] = sum of the B * n_sc chunk partials in chunk order; grid (H, 2), 256 threads x 32 values.
+// dW[h] = sum of the B * n_sc chunk partials in chunk order; one element per thread,
+// grid (128 * 64 / 256, H, 2).
 __global__ void __launch_bounds__(256) otf_bwd_wreduce_kernel(OtfBwdParams p) {
-  const int h = blockIdx.x, x = blockIdx.y;
+  const int h = blockIdx.y, x = blockIdx.z;
+  const int e = blockIdx.x * 256 + threadIdx.x;
   const int np = p.B * p.n_sc;
-  const float* part = p.wpart + ((size_t)x * p.H + h) * (size_t)np * (kIn * kLat);
-  void* dW = x ? p.dwv : p.dwk;
-  for (int e = threadIdx.x; e < kIn * kLat; e += 256) {
-    float acc = 0.f;
-    for (int j = 0; j < np; ++j) acc += part[(size_t)j * (kIn * kLat) + e];
-    const int64_t at = h * p.dw_sh + (e / kLat) * p.dw_si + (e % kLat);
-    if (p.dw_fp32) static_cast<float*>(dW)[at] = acc;
-    else static_cast<bf16*>(dW)[at] = (bf16)acc;
-  }
+  const float* part = p.wpart + ((size_t)x * p.H + h) * (size_t)np * (kIn * kLat) + e;
+  float acc = 0.f;
+  for (int j = 0; j < np; ++j) acc += part[(size_t)j * (kIn * kLat)];
+  const int64_t at = h * p.dw_sh + (e / kLat) * p.dw_si + (e % kLat);
+  if (p.dw_fp32) static_cast<float*>(x ? p.dwv : p.dwk)[at] = acc;
+  else static_cast<bf16*>(x ? p.dwv : p.dwk)[at] = (bf16)acc;
 }
 
 struct OtfBwdPlan {
   int Sqp, Skp, n_sc;
-  size_t off_q16, off_do16, off_lsed, off_klat, off_vlat, off_dklat, off_dvlat, off_wpart, bytes;
+  size_t off_q16, off_do16, off_lsed, off_klat, off_vlat, off_dklat, off_dvlat, off_wpart, off_wt, bytes;
 };
 
 OtfBwdPlan make_otf_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk) {
@@ -594,6 +619,7 @@ OtfBwdPlan make_otf_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk) {
   pl.off_dklat = o; o += up(keys * kLat * 2);
   pl.off_dvlat = o; o += up(keys * kLat * 2);
   pl.off_wpart = o; o += up((size_t)2 * H * B * pl.n_sc * kIn * kLat * sizeof(float));
+  pl.off_wt = o;    o += up((size_t)2 * H * kIn * kLat * 2);
   pl.bytes = o;
   return pl;
 }
@@ -693,14 +719,16 @@ extern "C" int dmla_bwd_onthefly(const void* q, const void* k, const void* v, co
   p.dklat = reinterpret_cast<_Float16*>(ws + pl.off_dklat);
   p.dvlat = reinterpret_cast<_Float16*>(ws + pl.off_dvlat);
   p.wpart = reinterpret_cast<float*>(ws + pl.off_wpart);
+  p.wt = reinterpret_cast<bf16*>(ws + pl.off_wt);
 
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(otf_bwd_prep_kernel, dim3((unsigned)(pl.Sqp / 32), (unsigned)(B * H)), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(otf_bwd_wt_kernel, dim3((unsigned)H, 2), dim3(256), 0, s, p);
   hipLaunchKernelGGL(otf_bwd_proj_kernel, dim3((unsigned)((pl.Skp + 255) / 256), (unsigned)H, (unsigned)B), dim3(256),
                      0, s, p);
   hipLaunchKernelGGL(otf_bwd_dkdv_kernel, dim3((unsigned)grid_kv), dim3(256), 0, s, p);
   hipLaunchKernelGGL(otf_bwd_dq_kernel, dim3((unsigned)grid_q), dim3(256), 0, s, p);
   hipLaunchKernelGGL(otf_bwd_wgrad_kernel, dim3((unsigned)pl.n_sc, (unsigned)H, (unsigned)(2 * B)), dim3(256), 0, s, p);
-  hipLaunchKernelGGL(otf_bwd_wreduce_kernel, dim3((unsigned)H, 2), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(otf_bwd_wreduce_kernel, dim3(kIn * kLat / 256, (unsigned)H, 2), dim3(256), 0, s, p);
   return check_launch("dmla_bwd_onthefly");
 }
