@@ -69,7 +69,8 @@ struct OtfBwdParams {
   float scale, scale_log2;
   _Float16* q16;         // [B*H][Sqp][64]; padding rows zero
   _Float16* do16;        // [B*H][Sqp][64]
-  float2* lsed;          // [B*H][Sqp]: (lse2, D); padding and empty rows (+inf, D)
+  float* lse2;           // [B*H][Sqp]: (m + ln l) log2(e); padding and empty rows +inf
+  float* nd;             // [B*H][Sqp]: -D = -rowsum(dO * O); padding rows 0
   _Float16* klat;        // [B*H][Skp][64]; padding keys zero
   _Float16* vlat;
   _Float16* dklat;       // [B*H][Skp][64]; padding keys zero
@@ -130,14 +131,14 @@ __global__ void __launch_bounds__(256) otf_bwd_prep_kernel(OtfBwdParams p) {
   dsum += __shfl_xor(dsum, 2);
   dsum += __shfl_xor(dsum, 4);
   if (c == 0) {
-    float2 v = make_float2(__builtin_inff(), 0.f);
+    float lse = __builtin_inff();   // P = 0 for padding rows and rows without keys
     if (r < p.Sq) {
       const int64_t idx = (int64_t)bh * p.Sq + r;
       const float lv = p.l[idx];
-      v.x = lv > 0.f ? p.m[idx] * kLog2e + __builtin_log2f(lv) : __builtin_inff();   // P = 0 for rows without keys
-      v.y = dsum;
+      if (lv > 0.f) lse = p.m[idx] * kLog2e + __builtin_log2f(lv);
     }
-    p.lsed[(size_t)bh * p.Sqp + r] = v;
+    p.lse2[(size_t)bh * p.Sqp + r] = lse;
+    p.nd[(size_t)bh * p.Sqp + r] = -dsum;
   }
 }
 
@@ -247,13 +248,16 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
   const int n_st = row_first >= p.Sq ? 0 : (p.Sq - rs0 + 63) / 64;
   const _Float16* qsrc = p.q16 + (size_t)bh * p.Sqp * kLat;
   const _Float16* dsrc = p.do16 + (size_t)bh * p.Sqp * kLat;
-  const float2* lsed = p.lsed + (size_t)bh * p.Sqp;
+  const float* lse2 = p.lse2 + (size_t)bh * p.Sqp;
+  const float* nd = p.nd + (size_t)bh * p.Sqp;
   const unsigned lbase = lds_addr(lds);
   const float sl2 = p.scale_log2;
 
   // One 32-row sub-tile; kMask applies the causal / key-range mask (only sub-tiles that reach
   // past some pair's limit need it), so the common case is straight-line code.
-  auto subtile = [&](const DMLA_LDS char* qt, const DMLA_LDS char* dt, int r0, const float4 (&e)[4], auto mask_tag) {
+  // dP - D comes straight out of the dP product: its accumulator starts at -D of the row.
+  auto subtile = [&](const DMLA_LDS char* qt, const DMLA_LDS char* dt, int r0, const f32x4 (&ls)[2],
+                     const f32x4 (&ndv)[2], auto mask_tag) {
     constexpr bool kMask = decltype(mask_tag)::value;
     f32x4 sacc[2][2], dpacc[2][2];   // [rb][kb]: rows 16 rb + 4 g + i, key 16 kb + l16
 #pragma unroll
@@ -266,28 +270,25 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
       for (int kb = 0; kb < 2; ++kb) {
         sacc[rb][kb] = mfma_f16(qa0, kreg[kb][0], f32x4{0.f, 0.f, 0.f, 0.f});
         sacc[rb][kb] = mfma_f16(qa1, kreg[kb][1], sacc[rb][kb]);
-        dpacc[rb][kb] = mfma_f16(oa0, vreg[kb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+        dpacc[rb][kb] = mfma_f16(oa0, vreg[kb][0], ndv[rb]);
         dpacc[rb][kb] = mfma_f16(oa1, vreg[kb][1], dpacc[rb][kb]);
       }
     }
     f16x8 pb[2], dsb[2];   // [kb]: B operands, slot 4 rb + i = row 16 rb + 4 g + i
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-      const float4 ea = e[2 * rb], eb = e[2 * rb + 1];
-      const float lse[4] = {ea.x, ea.z, eb.x, eb.z};
-      const float dd[4] = {ea.y, ea.w, eb.y, eb.w};
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float pv = fast_exp2(__builtin_fmaf(sacc[rb][kb][i], sl2, -lse[i]));
+          float pv = fast_exp2(__builtin_fmaf(sacc[rb][kb][i], sl2, -ls[rb][i]));
           if constexpr (kMask) {
             const int row = r0 + 16 * rb + 4 * g + i, key = k0 + 16 * kb + l16;
             const int lim = p.causal ? min(row + off, p.Sk - 1) : p.Sk - 1;
             pv = key > lim ? 0.f : pv;
           }
           pb[kb][4 * rb + i] = (_Float16)pv;
-          dsb[kb][4 * rb + i] = (_Float16)(pv * (dpacc[rb][kb][i] - dd[i]));
+          dsb[kb][4 * rb + i] = (_Float16)(pv * dpacc[rb][kb][i]);
         }
     }
 #pragma unroll
@@ -306,17 +307,17 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
   for (int s = 0; s < n_st; ++s) {
     wait_vmem();
     __syncthreads();   // stage s complete; every wave is done with stage s-1
-    // (lse2, D) of rows r0 + 16 rb + 4 g + i, four float2 = two float4 per row block; loaded
-    // before the next stage's copies so that waiting for them does not wait for the copies.
-    float4 e[2][4];
+    // lse2 and -D of rows r0 + 16 rb + 4 g + i, loaded before the next stage's copies so that
+    // waiting for them does not wait for the copies.
+    f32x4 ls[2][2], ndv[2][2];   // [t][rb]
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const float4* lp = reinterpret_cast<const float4*>(lsed + rs0 + 64 * s + 32 * t + 4 * g);
-      e[t][0] = lp[0];
-      e[t][1] = lp[1];
-      e[t][2] = lp[8];
-      e[t][3] = lp[9];
-    }
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        const int r = rs0 + 64 * s + 32 * t + 16 * rb + 4 * g;
+        ls[t][rb] = *reinterpret_cast<const f32x4*>(lse2 + r);
+        ndv[t][rb] = *reinterpret_cast<const f32x4*>(nd + r);
+      }
     if (s + 1 < n_st) stage_pair(qsrc, dsrc, rs0 + 64 * (s + 1), lbase + ((s + 1) & 1) * kStage, wave, lane);
     const DMLA_LDS char* st = lds + (s & 1) * kStage;
 #pragma unroll
@@ -324,9 +325,9 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
       const int r0 = rs0 + 64 * s + 32 * t;
       if (r0 >= p.Sq || (p.causal && k0 > r0 + 31 + off)) continue;   // padding only / all masked
       if (k0 + 31 >= p.Sk || (p.causal && k0 + 31 > r0 + off))
-        subtile(st + t * kTile, st + (2 + t) * kTile, r0, e[t], std::true_type{});
+        subtile(st + t * kTile, st + (2 + t) * kTile, r0, ls[t], ndv[t], std::true_type{});
       else
-        subtile(st + t * kTile, st + (2 + t) * kTile, r0, e[t], std::false_type{});
+        subtile(st + t * kTile, st + (2 + t) * kTile, r0, ls[t], ndv[t], std::false_type{});
     }
   }
   // dK_lat = scale dS^T Q and dV_lat = P^T dO as fp16 rows (keys past Sk hold zeros: P = 0 there)
@@ -367,7 +368,8 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
   const int off = p.Sk - p.Sq;
   const int r0 = rblk * kRowBlk + 32 * wave;
   f16x8 qreg[2][2], oreg[2][2];   // [rb][ks]: X16[r0 + 16 rb + l16][32 ks + 8 g ..]
-  float lse[2], dd[2];
+  float lse[2];
+  f32x4 ndv[2];   // -D of row r0 + 16 rb + l16 in all four elements: the dP^T accumulator start
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
     const size_t base = ((size_t)bh * p.Sqp + r0 + 16 * rb + l16) * kLat + 8 * g;
@@ -376,9 +378,9 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
       qreg[rb][ks] = *reinterpret_cast<const f16x8*>(p.q16 + base + 32 * ks);
       oreg[rb][ks] = *reinterpret_cast<const f16x8*>(p.do16 + base + 32 * ks);
     }
-    const float2 e = p.lsed[(size_t)bh * p.Sqp + r0 + 16 * rb + l16];
-    lse[rb] = e.x;
-    dd[rb] = e.y;
+    lse[rb] = p.lse2[(size_t)bh * p.Sqp + r0 + 16 * rb + l16];
+    const float n = p.nd[(size_t)bh * p.Sqp + r0 + 16 * rb + l16];
+    ndv[rb] = f32x4{n, n, n, n};
   }
   f32x4 dq[2][4];   // [rb][db]: dQ[r0 + 16 rb + 4 g + i][16 db + l16]
 #pragma unroll
@@ -406,7 +408,7 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
       for (int rb = 0; rb < 2; ++rb) {
         sT[kb][rb] = mfma_f16(ka0, qreg[rb][0], f32x4{0.f, 0.f, 0.f, 0.f});
         sT[kb][rb] = mfma_f16(ka1, qreg[rb][1], sT[kb][rb]);
-        dpT[kb][rb] = mfma_f16(va0, oreg[rb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+        dpT[kb][rb] = mfma_f16(va0, oreg[rb][0], ndv[rb]);
         dpT[kb][rb] = mfma_f16(va1, oreg[rb][1], dpT[kb][rb]);
       }
     }
@@ -423,7 +425,7 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
             const int lim = p.causal ? min(row + off, p.Sk - 1) : p.Sk - 1;
             pv = key > lim ? 0.f : pv;
           }
-          dsa[rb][4 * kb + i] = (_Float16)(pv * (dpT[kb][rb][i] - dd[rb]));
+          dsa[rb][4 * kb + i] = (_Float16)(pv * dpT[kb][rb][i]);
         }
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
@@ -600,7 +602,7 @@ __global__ void __launch_bounds__(256) otf_bwd_wreduce_kernel(OtfBwdParams p) {
 
 struct OtfBwdPlan {
   int Sqp, Skp, n_sc;
-  size_t off_q16, off_do16, off_lsed, off_klat, off_vlat, off_dklat, off_dvlat, off_wpart, off_wt, bytes;
+  size_t off_q16, off_do16, off_lse2, off_nd, off_klat, off_vlat, off_dklat, off_dvlat, off_wpart, off_wt, bytes;
 };
 
 OtfBwdPlan make_otf_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk) {
@@ -613,7 +615,8 @@ OtfBwdPlan make_otf_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk) {
   size_t o = 0;
   pl.off_q16 = o;   o += up(rows * kLat * 2);
   pl.off_do16 = o;  o += up(rows * kLat * 2);
-  pl.off_lsed = o;  o += up(rows * sizeof(float2));
+  pl.off_lse2 = o;  o += up(rows * sizeof(float));
+  pl.off_nd = o;    o += up(rows * sizeof(float));
   pl.off_klat = o;  o += up(keys * kLat * 2);
   pl.off_vlat = o;  o += up(keys * kLat * 2);
   pl.off_dklat = o; o += up(keys * kLat * 2);
@@ -713,7 +716,8 @@ extern "C" int dmla_bwd_onthefly(const void* q, const void* k, const void* v, co
   char* ws = static_cast<char*>(workspace);
   p.q16 = reinterpret_cast<_Float16*>(ws + pl.off_q16);
   p.do16 = reinterpret_cast<_Float16*>(ws + pl.off_do16);
-  p.lsed = reinterpret_cast<float2*>(ws + pl.off_lsed);
+  p.lse2 = reinterpret_cast<float*>(ws + pl.off_lse2);
+  p.nd = reinterpret_cast<float*>(ws + pl.off_nd);
   p.klat = reinterpret_cast<_Float16*>(ws + pl.off_klat);
   p.vlat = reinterpret_cast<_Float16*>(ws + pl.off_vlat);
   p.dklat = reinterpret_cast<_Float16*>(ws + pl.off_dklat);
