@@ -18,10 +18,11 @@
 // Every MFMA operand read from LDS is a conflict-free 16-byte read: K_lat rows for S^T and a
 // V_lat^T tile whose key order matches the C layout of S^T (so P needs no transposition).
 //
-// Softmax: scores are taken in log2 units against a per-row reference max m_ref that only moves
-// when a tile's max exceeds it by more than kSlack (p <= 2^kSlack in between); moving it
-// rescales O and l.  The exact running max is tracked beside it for the m / l outputs, which
+// Softmax: in log2 units against a per-row reference max m_ref that only moves when a tile's
+// max exceeds it by more than kSlack (p <= 2^kSlack in between); moving it rescales O and l.  The exact running max is tracked beside it for the m / l outputs, which
 // follow the cache-latent forward's convention (natural-log units).
+#include <type_traits>
+
 #include "dmla_common.h"
 #include "dmla_host.h"
 
@@ -148,32 +149,38 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
     wreg[ks] = *reinterpret_cast<const DMLA_LDS bf16x8*>(lds + kWOff + (pk ? 0 : kWBytes) +
                                                          raw_off(16 * pdb + l16, 4 * ks + g));
 
-  // Project tile t (raw stage st) into latent buffer lb.
+  // Project tile t (raw stage st) into latent buffer lb.  One wave-uniform branch for the
+  // whole projection (a select per MFMA compiles to a branch around every MFMA).
   auto project = [&](int st, int lb) {
-    const DMLA_LDS char* raw = lds + kRawOff + (st * 2 + (pk ? 0 : 1)) * kRawBytes;
-    DMLA_LDS char* lat = lds + kLatOff + (lb * 2 + (pk ? 0 : 1)) * kLatBytes;
+    auto proj = [&](auto is_k) {
+      constexpr bool kK = decltype(is_k)::value;
+      const DMLA_LDS char* raw = lds + kRawOff + (st * 2 + (kK ? 0 : 1)) * kRawBytes;
+      DMLA_LDS char* lat = lds + kLatOff + (lb * 2 + (kK ? 0 : 1)) * kLatBytes;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+      for (int kb = 0; kb < 4; ++kb) {
+        f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 x = *reinterpret_cast<const DMLA_LDS bf16x8*>(raw + raw_off(16 * kb + l16, 4 * ks + g));
-        c = pk ? mfma_bf16(wreg[ks], x, c)     // K_lat^T[dim 16 pdb + 4g + i][key 16 kb + l16]
-               : mfma_bf16(x, wreg[ks], c);    // V_lat[key 16 kb + 4g + i][dim 16 pdb + l16]
+        for (int ks = 0; ks < 4; ++ks) {
+          const bf16x8 x = *reinterpret_cast<const DMLA_LDS bf16x8*>(raw + raw_off(16 * kb + l16, 4 * ks + g));
+          if constexpr (kK) c = mfma_bf16(wreg[ks], x, c);   // K_lat^T[dim 16 pdb + 4g + i][key 16 kb + l16]
+          else c = mfma_bf16(x, wreg[ks], c);                // V_lat[key 16 kb + 4g + i][dim 16 pdb + l16]
+        }
+        f16x4 v;
+        v[0] = (_Float16)c[0]; v[1] = (_Float16)c[1]; v[2] = (_Float16)c[2]; v[3] = (_Float16)c[3];
+        if constexpr (kK) {
+          // K_lat[key 16 kb + l16][dims 16 pdb + 4g .. +3]
+          const int key = 16 * kb + l16;
+          *reinterpret_cast<DMLA_LDS f16x4*>(lat + lat_off(key, 2 * pdb + (g >> 1)) + 8 * (g & 1)) = v;
+        } else {
+          // V_lat^T[dim 16 pdb + l16][position]: keys 4g + i of key block kb sit at positions
+          // 32 (kb/2) + 8 g + 4 (kb&1) + i, the key order of the P operand (S^T C layout).
+          const int dim = 16 * pdb + l16;
+          *reinterpret_cast<DMLA_LDS f16x4*>(lat + lat_off(dim, 4 * (kb >> 1) + g) + 8 * (kb & 1)) = v;
+        }
       }
-      f16x4 v;
-      v[0] = (_Float16)c[0]; v[1] = (_Float16)c[1]; v[2] = (_Float16)c[2]; v[3] = (_Float16)c[3];
-      if (pk) {
-        // K_lat[key 16 kb + l16][dims 16 pdb + 4g .. +3]
-        const int key = 16 * kb + l16;
-        *reinterpret_cast<DMLA_LDS f16x4*>(lat + lat_off(key, 2 * pdb + (g >> 1)) + 8 * (g & 1)) = v;
-      } else {
-        // V_lat^T[dim 16 pdb + l16][position]: keys 4g + i of key block kb sit at positions
-        // 32 (kb/2) + 8 g + 4 (kb&1) + i, the key order of the P operand (S^T C layout).
-        const int dim = 16 * pdb + l16;
-        *reinterpret_cast<DMLA_LDS f16x4*>(lat + lat_off(dim, 4 * (kb >> 1) + g) + 8 * (kb & 1)) = v;
-      }
-    }
+    };
+    if (pk) proj(std::true_type{});
+    else proj(std::false_type{});
   };
 
   f32x4 oacc[4][4];   // O[row0 + 16 rb + 4 g + i][16 db + l16]
@@ -212,34 +219,30 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
         s[kb][rb] = mfma_f16(k1, qreg[rb][1], s[kb][rb]);
       }
     }
-    // Scale to log2 units and mask (only tiles that reach past some row's limit or past Sk).
+    // Scores stay unscaled (scale > 0 keeps their order): the tile max is taken on them and the
+    // scale folds into the exp2 argument.  Only tiles that reach past some row's limit or past
+    // Sk are masked, in a block of their own.
     const int key0 = t * kOtfKeys;
-    const bool need_mask = key0 + kOtfKeys > p.Sk || (p.causal && key0 + kOtfKeys - 1 > row0 + off);
+    if (key0 + kOtfKeys > p.Sk || (p.causal && key0 + kOtfKeys - 1 > row0 + off)) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+      for (int rb = 0; rb < 4; ++rb) {
+        const int lim = p.causal ? min(own_pos0 + 16 * rb + off, p.Sk - 1) : p.Sk - 1;
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb)
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float x = s[kb][rb][i] * sl2;
-          if (need_mask) {
-            const int key = key0 + 16 * kb + 4 * g + i;
-            const int lim = p.causal ? min(own_pos0 + 16 * rb + off, p.Sk - 1) : p.Sk - 1;
-            if (key > lim) x = kNegInf;
-          }
-          s[kb][rb][i] = x;
-        }
-    // Tile max per own row (lane-partial), exact running max, and the slack test.
+          for (int i = 0; i < 4; ++i)
+            if (key0 + 16 * kb + 4 * g + i > lim) s[kb][rb][i] = kNegInf;
+      }
+    }
+    // Tile max per own row (lane-partial, log2 units), exact running max, and the slack test.
     bool raise = false;
-    float tmax[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       float mx = kNegInf;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kb][rb][i]);
-      tmax[rb] = mx;
+        mx = fmaxf(mx, fmaxf(fmaxf(s[kb][rb][0], s[kb][rb][1]), fmaxf(s[kb][rb][2], s[kb][rb][3])));
+      mx *= sl2;
       mtrue[rb] = fmaxf(mtrue[rb], mx);
       raise |= mx > mref[rb] + kSlack;
     }
@@ -261,17 +264,17 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
         }
       }
     }
-    // P = exp2(s - mref) (0 for masked keys and for rows without a finite reference yet).
+    // P = exp2(s scale - mref) (0 for masked keys and for rows without a finite reference yet).
     f16x8 pa[4][2];   // A operand of O += P V_lat: [rb][ks], keys of k-step ks in V_lat^T order
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
-      const float mr = mref[rb] == kNegInf ? 0.f : mref[rb];
+      const float nmr = mref[rb] == kNegInf ? 0.f : -mref[rb];
       float ps = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float e = fast_exp2(s[kb][rb][i] - mr);
+          const float e = fast_exp2(__builtin_fmaf(s[kb][rb][i], sl2, nmr));
           ps += e;
           pa[rb][kb >> 1][4 * (kb & 1) + i] = (_Float16)e;
         }
