@@ -303,8 +303,10 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
     }
   };
 
-  if (n_st > 0) stage_pair(qsrc, dsrc, rs0, lbase, wave, lane);
-  for (int s = 0; s < n_st; ++s) {
+  // One stage; the buffer index is a compile-time constant (the loop below is unrolled by two)
+  // so that every LDS address is a lane offset plus an instruction immediate.
+  auto stage_iter = [&](int s, auto buf_tag) {
+    constexpr int kBuf = decltype(buf_tag)::value;
     wait_vmem();
     __syncthreads();   // stage s complete; every wave is done with stage s-1
     // lse2 and -D of rows r0 + 16 rb + 4 g + i, loaded before the next stage's copies so that
@@ -318,8 +320,8 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
         ls[t][rb] = *reinterpret_cast<const f32x4*>(lse2 + r);
         ndv[t][rb] = *reinterpret_cast<const f32x4*>(nd + r);
       }
-    if (s + 1 < n_st) stage_pair(qsrc, dsrc, rs0 + 64 * (s + 1), lbase + ((s + 1) & 1) * kStage, wave, lane);
-    const DMLA_LDS char* st = lds + (s & 1) * kStage;
+    if (s + 1 < n_st) stage_pair(qsrc, dsrc, rs0 + 64 * (s + 1), lbase + (1 - kBuf) * kStage, wave, lane);
+    const DMLA_LDS char* st = lds + kBuf * kStage;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int r0 = rs0 + 64 * s + 32 * t;
@@ -329,6 +331,11 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
       else
         subtile(st + t * kTile, st + (2 + t) * kTile, r0, ls[t], ndv[t], std::false_type{});
     }
+  };
+  if (n_st > 0) stage_pair(qsrc, dsrc, rs0, lbase, wave, lane);
+  for (int s = 0; s < n_st; s += 2) {
+    stage_iter(s, std::integral_constant<int, 0>{});
+    if (s + 1 < n_st) stage_iter(s + 1, std::integral_constant<int, 1>{});
   }
   // dK_lat = scale dS^T Q and dV_lat = P^T dO as fp16 rows (keys past Sk hold zeros: P = 0 there)
 #pragma unroll
@@ -435,12 +442,13 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
     }
   };
 
-  if (n_st > 0) stage_pair(ksrc, vsrc, 0, lbase, wave, lane);
-  for (int s = 0; s < n_st; ++s) {
+  // Unrolled by two stages so that the buffer offset is an instruction immediate.
+  auto stage_iter = [&](int s, auto buf_tag) {
+    constexpr int kBuf = decltype(buf_tag)::value;
     wait_vmem();
     __syncthreads();
-    if (s + 1 < n_st) stage_pair(ksrc, vsrc, 64 * (s + 1), lbase + ((s + 1) & 1) * kStage, wave, lane);
-    const DMLA_LDS char* st = lds + (s & 1) * kStage;
+    if (s + 1 < n_st) stage_pair(ksrc, vsrc, 64 * (s + 1), lbase + (1 - kBuf) * kStage, wave, lane);
+    const DMLA_LDS char* st = lds + kBuf * kStage;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int c0 = 64 * s + 32 * t;
@@ -450,6 +458,11 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
       else
         subtile(st + t * kTile, st + (2 + t) * kTile, c0, std::false_type{});
     }
+  };
+  if (n_st > 0) stage_pair(ksrc, vsrc, 0, lbase, wave, lane);
+  for (int s = 0; s < n_st; s += 2) {
+    stage_iter(s, std::integral_constant<int, 0>{});
+    if (s + 1 < n_st) stage_iter(s + 1, std::integral_constant<int, 1>{});
   }
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
