@@ -54,7 +54,14 @@ __global__ void __launch_bounds__(128) lse_combine_kernel(CombineArgs a) {
       const float lv = a.part_lse[lbase + (int64_t)s * a.lse_ss];
       if (lv == kNegInf) continue;   // an empty split may hold anything in its o slot
       const float w = __expf(lv - mref);
-      acc += w * *reinterpret_cast<const f32x4*>(a.part_o + obase + (int64_t)s * a.po_ss + col);
+      f32x4 v;
+      if (a.part_o16 != nullptr) {
+        const bf16x4 x = *reinterpret_cast<const bf16x4*>(a.part_o16 + obase + (int64_t)s * a.po_ss + col);
+        v = f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+      } else {
+        v = *reinterpret_cast<const f32x4*>(a.part_o + obase + (int64_t)s * a.po_ss + col);
+      }
+      acc += w * v;
     }
     acc *= inv;
     bf16x4 w4;

@@ -108,7 +108,7 @@ struct MqaParams {
   int head_groups;     // ceil(H / 64)
   int n_ranges;        // R of the decode plan
   const int32_t* plan; // decode plan (see decode_plan_kernel)
-  float* part_o;       // [slots, H, 512] normalised partial outputs
+  bf16* part_o;        // [slots, H, 512] normalised partial outputs, rounded to bf16
   float* part_lse;     // [slots, H]
 };
 
@@ -606,12 +606,16 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
         *reinterpret_cast<bf16x4*>(orp + 16 * d) = w;
       }
     } else {
-      float* pp = p.part_o + ((int64_t)wk.slot * p.H + r) * kDv + col;
+      // bf16 partials: the end-of-segment stores of all workgroups come in one burst that the
+      // HBM write bandwidth paces; the combine rescales and sums them in fp32.
+      bf16* pp = p.part_o + ((int64_t)wk.slot * p.H + r) * kDv + col;
 #pragma unroll
       for (int d = 0; d < kDbWave; ++d) {
         f32x4 v = oacc[d][qg] * inv;
         if (poison) v = f32x4{nanv, nanv, nanv, nanv};
-        *reinterpret_cast<f32x4*>(pp + 16 * d) = v;
+        bf16x4 w;
+        w[0] = (bf16)v[0]; w[1] = (bf16)v[1]; w[2] = (bf16)v[2]; w[3] = (bf16)v[3];
+        *reinterpret_cast<bf16x4*>(pp + 16 * d) = w;
       }
     }
   }
@@ -915,7 +919,7 @@ static int64_t decode_slots(int64_t B, int64_t H, int64_t max_pages_per_seq) {
 extern "C" int64_t dmla_decode_workspace_bytes(int64_t B, int64_t H, int64_t d_v, int64_t max_pages_per_seq) {
   if (B <= 0 || H <= 0 || d_v != kDv || max_pages_per_seq <= 0) return 0;
   return dmla_decode_plan_bytes(B, H, max_pages_per_seq) +
-         decode_slots(B, H, max_pages_per_seq) * H * (int64_t)(kDv + 1) * (int64_t)sizeof(float);
+         decode_slots(B, H, max_pages_per_seq) * H * (int64_t)(kDv * 2 + 4);
 }
 
 extern "C" int dmla_decode_plan(const int32_t* cache_seqlens, int64_t B, int64_t H, int64_t max_pages_per_seq,
@@ -983,7 +987,7 @@ extern "C" int dmla_decode_paged_planned(const void* q, const void* kv_pool, con
                             max_pages_per_seq, q_sb, q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale);
   if (rc0 != DMLA_OK || B == 0 || H == 0) return rc0;
   const int64_t slots = decode_slots(B, H, max_pages_per_seq);
-  const int64_t need = slots * H * (int64_t)(kDv + 1) * (int64_t)sizeof(float);
+  const int64_t need = slots * H * (int64_t)(kDv * 2 + 4);   // bf16 partial rows, then fp32 lse
   if (workspace == nullptr || workspace_bytes < need)
     return fail(DMLA_ERR_WORKSPACE, "dmla_decode_paged: workspace of %lld bytes needed (got %lld)",
                 (long long)need, (long long)workspace_bytes);
@@ -1007,8 +1011,8 @@ extern "C" int dmla_decode_paged_planned(const void* q, const void* kv_pool, con
   p.head_groups = (int)((H + kRowsPerWG - 1) / kRowsPerWG);
   p.n_ranges = (int)decode_ranges(B, H, max_pages_per_seq);
   p.plan = plan;
-  p.part_o = static_cast<float*>(workspace);
-  p.part_lse = p.part_o + slots * H * kDv;
+  p.part_o = static_cast<bf16*>(workspace);
+  p.part_lse = reinterpret_cast<float*>(p.part_o + slots * H * kDv);
   const int64_t grid = ((int64_t)(p.n_ranges + 7) / 8) * 8 * p.head_groups;
   if (grid > 0x7fffffff) return fail(DMLA_ERR_UNSUPPORTED, "dmla_decode_paged: grid too large");
   hipLaunchKernelGGL(mqa_fwd_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream, p);
@@ -1018,7 +1022,7 @@ extern "C" int dmla_decode_paged_planned(const void* q, const void* kv_pool, con
   // ones: zeros, lse -inf) come from the combine.
   const int32_t* tile_prefix = plan + kPlanHeader;
   CombineArgs c = {};
-  c.part_o = p.part_o;
+  c.part_o16 = p.part_o;
   c.part_lse = p.part_lse;
   c.split_base = tile_prefix + B + 1;
   c.num_splits = tile_prefix + 2 * (B + 1);

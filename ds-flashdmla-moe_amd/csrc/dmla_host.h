@@ -29,8 +29,10 @@ int device_cu_count();
 // sequence b is at b * sb + s * ss, or at (split_base[b] + s) * ss when split_base is given.
 // skip_single leaves sequences with one split untouched (their rows were written by the
 // producer directly).
+// part_o16, when set, replaces part_o with bf16 partials of the same layout (the decode's own).
 struct CombineArgs {
   const float* part_o;
+  const __bf16* part_o16;
   const float* part_lse;
   const int32_t* num_splits;
   const int32_t* split_base;
