@@ -202,8 +202,10 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
   for (int t = 0; t < n_t; ++t) {
     wait_vmem();
     __syncthreads();   // latent tile t written, raw tile t+1 landed, raw stage t%2 and latent buffer (t+1)%2 free
-    if (t + 2 < n_t) stage_raw(t + 2, t & 1);
     if (t + 1 < n_t) project((t + 1) & 1, (t + 1) & 1);
+    // Tile t+2's raw copies go out after the projection: issued straight after the barrier, the
+    // 32 KB of copies of all waves queue in the CU's vector-memory path ahead of the work.
+    if (t + 2 < n_t) stage_raw(t + 2, t & 1);
 
     const DMLA_LDS char* klat = lds + kLatOff + ((t & 1) * 2) * kLatBytes;
     const DMLA_LDS char* vlat = klat + kLatBytes;
