@@ -4,18 +4,112 @@
 //   * the split-KV log-sum-exp combine, also usable on its own (e.g. to merge partials that
 //     several devices computed over disjoint page ranges of one context).
 // Neither has a reference counterpart: the reference has no paged decode.
+#include <type_traits>
+
 #include "dmla_common.h"
 #include "dmla_host.h"
 
 namespace dmla {
 
 // ---- split-KV combine --------------------------------------------------------------------
-// One 128-thread block per (sequence, head); 4 columns per thread and pass.
+// One wave per (sequence, head), four per 256-thread block; lane l covers columns 4l + 256i.
 //   o = sum_s w_s o_s / sum_s w_s, w_s = exp(lse_s - max_s lse_s), lse = max + log(sum w)
 // over the first n_b splits; no finite lse leaves o = 0 and lse = -inf (max of the inputs);
-// a NaN lse makes o and lse NaN.
-__global__ void __launch_bounds__(128) lse_combine_kernel(CombineArgs a) {
-  const int b = blockIdx.x / a.H, h = blockIdx.x % a.H;
+// a NaN lse makes o and lse NaN.  A split with lse = -inf is skipped whatever its o slot holds.
+// The weights are summed and applied in split order.  The common decode shape (at most 4
+// splits, d <= 512) issues every partial load before the first weight is known, so a wave
+// waits for one memory round trip instead of one per phase.
+constexpr int kCombineFast = 4;   // splits held in registers by the one-round-trip path
+
+template <typename T>
+__device__ __forceinline__ f32x4 load_part4(const T* p) {
+  if constexpr (std::is_same<T, float>::value) {
+    return *reinterpret_cast<const f32x4*>(p);
+  } else {
+    const bf16x4 x = *reinterpret_cast<const bf16x4*>(p);
+    return f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void combine_pair(const CombineArgs& a, const T* part, int b, int h, int n, int lane) {
+  const int64_t s0 = a.split_base != nullptr ? (int64_t)a.split_base[b] : 0;
+  const int64_t lbase = (a.split_base != nullptr ? s0 * a.lse_ss : (int64_t)b * a.lse_sb) + (int64_t)h * a.lse_sh;
+  const int64_t obase = (a.split_base != nullptr ? s0 * a.po_ss : (int64_t)b * a.po_sb) + (int64_t)h * a.po_sh;
+  bf16* orow = a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+  // lse of split s < 64 sits in lane s; later splits are read again from memory
+  const float lv_lane = lane < n ? a.part_lse[lbase + (int64_t)lane * a.lse_ss] : kNegInf;
+  auto lse_of = [&](int s) -> float {
+    if (s < 64) return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lv_lane), s));
+    return a.part_lse[lbase + (int64_t)s * a.lse_ss];
+  };
+  const bool fast = n >= 1 && n <= kCombineFast && a.d <= 512;
+  f32x4 pre[kCombineFast][2];
+  if (fast) {
+    // Unconditional loads (split 0 and column 0 stand in for the ones that do not exist), so
+    // that all of them are in flight together; the extra values are never used.
+#pragma unroll
+    for (int s = 0; s < kCombineFast; ++s)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int col = 4 * lane + 256 * i;
+        pre[s][i] = load_part4(part + obase + (int64_t)(s < n ? s : 0) * a.po_ss + (col < a.d ? col : 0));
+      }
+  }
+  float mx = kNegInf;
+  bool bad = false;   // a NaN lse (e.g. a split that met an invalid page) poisons the sequence
+  for (int s = 0; s < n; ++s) {
+    const float lv = lse_of(s);
+    bad = bad || lv != lv;
+    mx = fmaxf(mx, lv);
+  }
+  if (bad) {
+    const bf16 nb = (bf16)__builtin_nanf("");
+    for (int col = 4 * lane; col < a.d; col += 256) *reinterpret_cast<bf16x4*>(orow + col) = bf16x4{nb, nb, nb, nb};
+    if (lane == 0 && a.lse != nullptr) a.lse[(int64_t)b * a.H + h] = __builtin_nanf("");
+    return;
+  }
+  const float mref = mx == kNegInf ? 0.f : mx;
+  float wsum = 0.f;
+  for (int s = 0; s < n; ++s) wsum += __expf(lse_of(s) - mref);
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  auto store = [&](int col, f32x4 acc) {
+    acc *= inv;
+    bf16x4 w4;
+    w4[0] = (bf16)acc[0]; w4[1] = (bf16)acc[1]; w4[2] = (bf16)acc[2]; w4[3] = (bf16)acc[3];
+    *reinterpret_cast<bf16x4*>(orow + col) = w4;
+  };
+  if (fast) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int col = 4 * lane + 256 * i;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < kCombineFast; ++s) {
+        const float lv = lse_of(s);
+        if (s < n && lv != kNegInf) acc += __expf(lv - mref) * pre[s][i];
+      }
+      if (col < a.d) store(col, acc);
+    }
+  } else {
+    for (int col = 4 * lane; col < a.d; col += 256) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < n; ++s) {
+        const float lv = lse_of(s);
+        if (lv == kNegInf) continue;
+        acc += __expf(lv - mref) * load_part4(part + obase + (int64_t)s * a.po_ss + col);
+      }
+      store(col, acc);
+    }
+  }
+  if (lane == 0 && a.lse != nullptr) a.lse[(int64_t)b * a.H + h] = wsum > 0.f ? mref + __logf(wsum) : mx;
+}
+
+__global__ void __launch_bounds__(256) lse_combine_kernel(CombineArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t pair = (int64_t)blockIdx.x * 4 + uniform(threadIdx.x >> 6);
+  if (pair >= (int64_t)a.B * a.H) return;
+  const int b = (int)(pair / a.H), h = (int)(pair - (int64_t)b * a.H);
   int n = a.max_splits;
   if (a.num_splits != nullptr) {
     n = min(max(a.num_splits[b], 0), a.max_splits);
@@ -25,55 +119,13 @@ __global__ void __launch_bounds__(128) lse_combine_kernel(CombineArgs a) {
     n = max(1, (npages + a.pages_per_split - 1) / a.pages_per_split);
   }
   if (a.skip_single && n == 1) return;   // the decode kernel already wrote such rows itself
-  const int64_t s0 = a.split_base != nullptr ? (int64_t)a.split_base[b] : 0;
-  const int64_t lbase = (a.split_base != nullptr ? s0 * a.lse_ss : (int64_t)b * a.lse_sb) + (int64_t)h * a.lse_sh;
-  float mx = kNegInf;
-  bool bad = false;   // a NaN lse (e.g. a split that met an invalid page) poisons the sequence
-  for (int s = 0; s < n; ++s) {
-    const float lv = a.part_lse[lbase + (int64_t)s * a.lse_ss];
-    bad = bad || lv != lv;
-    mx = fmaxf(mx, lv);
-  }
-  if (bad) {
-    const float nanv = __builtin_nanf("");
-    for (int col = 4 * threadIdx.x; col < a.d; col += 4 * blockDim.x) {
-      const bf16 nb = (bf16)nanv;
-      *reinterpret_cast<bf16x4*>(a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + col) = bf16x4{nb, nb, nb, nb};
-    }
-    if (threadIdx.x == 0 && a.lse != nullptr) a.lse[(int64_t)b * a.H + h] = nanv;
-    return;
-  }
-  const float mref = mx == kNegInf ? 0.f : mx;
-  float wsum = 0.f;
-  for (int s = 0; s < n; ++s) wsum += __expf(a.part_lse[lbase + (int64_t)s * a.lse_ss] - mref);
-  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  const int64_t obase = (a.split_base != nullptr ? s0 * a.po_ss : (int64_t)b * a.po_sb) + (int64_t)h * a.po_sh;
-  for (int col = 4 * threadIdx.x; col < a.d; col += 4 * blockDim.x) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < n; ++s) {
-      const float lv = a.part_lse[lbase + (int64_t)s * a.lse_ss];
-      if (lv == kNegInf) continue;   // an empty split may hold anything in its o slot
-      const float w = __expf(lv - mref);
-      f32x4 v;
-      if (a.part_o16 != nullptr) {
-        const bf16x4 x = *reinterpret_cast<const bf16x4*>(a.part_o16 + obase + (int64_t)s * a.po_ss + col);
-        v = f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
-      } else {
-        v = *reinterpret_cast<const f32x4*>(a.part_o + obase + (int64_t)s * a.po_ss + col);
-      }
-      acc += w * v;
-    }
-    acc *= inv;
-    bf16x4 w4;
-    w4[0] = (bf16)acc[0]; w4[1] = (bf16)acc[1]; w4[2] = (bf16)acc[2]; w4[3] = (bf16)acc[3];
-    *reinterpret_cast<bf16x4*>(a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + col) = w4;
-  }
-  if (threadIdx.x == 0 && a.lse != nullptr) a.lse[(int64_t)b * a.H + h] = wsum > 0.f ? mref + __logf(wsum) : mx;
+  if (a.part_o16 != nullptr) combine_pair(a, a.part_o16, b, h, n, lane);
+  else combine_pair(a, a.part_o, b, h, n, lane);
 }
 
 int launch_lse_combine(const CombineArgs& a, hipStream_t stream, const char* what) {
   if (a.B == 0 || a.H == 0) return DMLA_OK;
-  hipLaunchKernelGGL(lse_combine_kernel, dim3((unsigned)(a.B * a.H)), dim3(128), 0, stream, a);
+  hipLaunchKernelGGL(lse_combine_kernel, dim3((unsigned)(((int64_t)a.B * a.H + 3) / 4)), dim3(256), 0, stream, a);
   return check_launch(what);
 }
 

@@ -708,9 +708,11 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
 // the binary searches read are mirrored in LDS when they fit (the common case), so every
 // dependent step is an LDS access rather than a global memory round trip.
 constexpr int kPlanLds = 4096;
-__global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlens, int B, int R, int max_pages,
+constexpr int kPlanThreads = 256;   // four waves: the scans and barriers stay short
+constexpr int kPlanWaves = kPlanThreads / 64;
+__global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const int32_t* seqlens, int B, int R, int max_pages,
                                                            int32_t* plan) {
-  __shared__ int scan[1024];
+  __shared__ int scan[kPlanThreads];
   __shared__ int l_tp[kPlanLds], l_ne[kPlanLds], l_rs[kPlanLds];
   int32_t* tile_prefix = plan + kPlanHeader;
   int32_t* split_base = tile_prefix + B + 1;
@@ -724,9 +726,9 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlen
   const int* ne = lds_b ? l_ne : num_splits;
   const int* rs = lds_r ? l_rs : range_start;
   const int tid = threadIdx.x;
-  // Prefix over 1024-element chunks: a shuffle scan within each wave, the 16 wave totals
-  // scanned by wave 0 through LDS, two barriers per chunk.  Returns the inclusive scan;
-  // scan[1023] is the chunk total afterwards.
+  // Prefix over kPlanThreads-element chunks: a shuffle scan within each wave, the wave totals
+  // scanned by wave 0 through LDS, three barriers per chunk.  Returns the inclusive scan;
+  // scan[kPlanThreads - 1] is the chunk total afterwards.
   auto chunk_scan = [&](int v) -> int {
     const int ln = tid & 63, wv = tid >> 6;
 #pragma unroll
@@ -737,33 +739,33 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlen
     if (ln == 63) scan[wv] = v;
     __syncthreads();
     if (wv == 0) {
-      int t = ln < 16 ? scan[ln] : 0;
+      int t = ln < kPlanWaves ? scan[ln] : 0;
 #pragma unroll
-      for (int off = 1; off < 16; off *= 2) {
+      for (int off = 1; off < kPlanWaves; off *= 2) {
         const int up = __shfl_up(t, off, 64);
         if (ln >= off) t += up;
       }
-      if (ln < 16) scan[32 + ln] = t;   // inclusive wave-total prefix
+      if (ln < kPlanWaves) scan[32 + ln] = t;   // inclusive wave-total prefix
     }
     __syncthreads();
     const int incl = v + (wv > 0 ? scan[32 + wv - 1] : 0);
-    if (tid == 1023) scan[1023] = incl;
+    if (tid == kPlanThreads - 1) scan[kPlanThreads - 1] = incl;
     __syncthreads();
     return incl;
   };
   int carry = 0, ncarry = 0;
-  for (int base = 0; base < B; base += 1024) {
+  for (int base = 0; base < B; base += kPlanThreads) {
     const int b = base + tid;
     int nt = 0;
     if (b < B) nt = (min(max(seqlens[b], 0), max_pages * kPage) + kTileN - 1) / kTileN;
     const int incl = chunk_scan(nt);
     const int tpb = carry + incl - nt;
-    carry += scan[1023];
+    carry += scan[kPlanThreads - 1];
     __syncthreads();
     const int nz = nt > 0 ? 1 : 0;
     const int incl2 = chunk_scan(nz);
     const int neb = ncarry + incl2 - nz;
-    ncarry += scan[1023];
+    ncarry += scan[kPlanThreads - 1];
     if (b < B) {
       tile_prefix[b] = tpb; num_splits[b] = neb;
       if (lds_b) { l_tp[b] = tpb; l_ne[b] = neb; }
@@ -778,7 +780,7 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlen
   __syncthreads();
   // Range starts: weighted position r W -> the sequence holding it (last b whose weighted start
   // is <= it) -> its tile, or the sequence's first tile when among its virtual tiles.
-  for (int r = tid; r <= R; r += 1024) {
+  for (int r = tid; r <= R; r += kPlanThreads) {
     int t = total;
     if (r < R && (int64_t)r * W < weighted) {
       const int64_t pos = (int64_t)r * W;
@@ -807,7 +809,7 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlen
     return lo;
   };
   int scarry = 0;
-  for (int base = 0; base < B; base += 1024) {
+  for (int base = 0; base < B; base += kPlanThreads) {
     const int b = base + tid;
     int ns = 0, fr = 0;
     if (b < B) {
@@ -821,7 +823,7 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlen
     if (b < B) { num_splits[b] = ns; first_range[b] = fr; }
     const int incl = chunk_scan(ns);
     if (b < B) split_base[b] = scarry + incl - ns;
-    scarry += scan[1023];
+    scarry += scan[kPlanThreads - 1];
     __syncthreads();
   }
   if (tid == 0) {
@@ -830,7 +832,7 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(const int32_t* seqlen
     plan[6] = plan[7] = 0;
   }
   // range_first_b[r]: the sequence holding tile range_start[r] (last b with tile_prefix[b] <= it)
-  for (int r = tid; r < R; r += 1024) {
+  for (int r = tid; r < R; r += kPlanThreads) {
     const int t = rs[r];
     int lo = 0, hi = B - 1;
     while (lo < hi) {
@@ -936,7 +938,7 @@ extern "C" int dmla_decode_plan(const int32_t* cache_seqlens, int64_t B, int64_t
     return fail(DMLA_ERR_WORKSPACE, "dmla_decode_plan: %lld bytes needed (got %lld)", (long long)need,
                 (long long)plan_bytes);
   const int64_t R = decode_ranges(B, H, max_pages_per_seq);
-  hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, cache_seqlens, (int)B, (int)R,
+  hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, cache_seqlens, (int)B, (int)R,
                      (int)max_pages_per_seq, plan);
   return check_launch("dmla_decode_plan");
 }
