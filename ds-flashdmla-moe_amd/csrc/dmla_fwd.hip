@@ -376,6 +376,16 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     return fmaxf(v, rowx[(slot * 2 + (kh ^ 1)) * kRowsPerWG + 16 * rb + l16]);
   };
 
+  // This wave's row statistics over its key half (l and the exact max of its own 16 rows),
+  // posted for the partner wave before the last barrier of the loop.
+  float lhalf = 0.f, mhalf = kNegInf;
+  auto post_row_stats = [&]() {
+    lhalf = group_sum(lsum);
+    mhalf = group_max(mtrue);
+    rowx[(2 * 2 + kh) * kRowsPerWG + 16 * rb + l16] = lhalf;
+    rowx[(0 * 2 + kh) * kRowsPerWG + 16 * rb + l16] = mhalf;
+  };
+
   f32x4 sacc[2];
 #pragma unroll
   for (int d = 0; d < kDbWave; ++d)
@@ -512,9 +522,12 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     for (; t + 2 < tile_end; ++t) iteration(t, std::integral_constant<int, 0>{});
     if (t + 1 < tile_end) iteration(t++, std::integral_constant<int, 1>{});
     iteration(t, std::integral_constant<int, 2>{});
+    post_row_stats();
     if constexpr (!kExact) flags[wave] = __any(overflow) ? 1 : 0;
     wait_vmem();
-    __syncthreads();     // P(end-1) and the overflow flags posted
+    // lgkmcnt(0): this wave's reads of the ring are done before any wave stages its output there
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __syncthreads();     // P(end-1), the row statistics and the overflow flags posted
     if constexpr (!kExact) {
       const i32x4 f0 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags);
       const i32x4 f1 = *reinterpret_cast<const DMLA_LDS i32x4*>(flags + 4);
@@ -524,22 +537,24 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
       }
     }
     pv(tile_end - 1);
+  } else {
+    post_row_stats();
+    __syncthreads();
   }
 
   // ---- epilogue ---------------------------------------------------------------------------
-  // Row statistics over both key halves, then 1/l of all 64 rows for the output scaling.
+  // Row statistics over both key halves, and 1/l of the 64 rows this wave scales (rows
+  // 16 qg + l16), read from the statistics both key-half waves posted.
   const bool poison = kDecode && __any(bad_page);
   const float nanv = __builtin_nanf("");
-  const float lhalf = group_sum(lsum);
-  const float mhalf = group_max(mtrue);
-  rowx[(2 * 2 + kh) * kRowsPerWG + 16 * rb + l16] = lhalf;
-  rowx[(0 * 2 + kh) * kRowsPerWG + 16 * rb + l16] = mhalf;
-  __syncthreads();
   const float ltot = lhalf + rowx[(2 * 2 + (kh ^ 1)) * kRowsPerWG + 16 * rb + l16];
   const float mt = fmaxf(mhalf, rowx[(0 * 2 + (kh ^ 1)) * kRowsPerWG + 16 * rb + l16]);
-  __syncthreads();
-  DMLA_LDS float* inv_l = rowx + 1 * 2 * kRowsPerWG;  // [64 rows]
-  if (kh == 0) inv_l[16 * rb + l16] = ltot > 0.f ? 1.f / ltot : 0.f;
+  float inv_l[4];
+#pragma unroll
+  for (int qg = 0; qg < 4; ++qg) {
+    const float lr = rowx[(2 * 2 + 0) * kRowsPerWG + 16 * qg + l16] + rowx[(2 * 2 + 1) * kRowsPerWG + 16 * qg + l16];
+    inv_l[qg] = lr > 0.f ? 1.f / lr : 0.f;
+  }
   if (kh == 0 && g == 0 && own_row < nrows) {
     if constexpr (!kDecode) {
       if (p.m != nullptr) {
@@ -557,7 +572,6 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
       }
     }
   }
-  __syncthreads();
   const int col = 64 * wave + 4 * g;
   if constexpr (!kDecode) {
     // O goes out as whole 1 KB rows: each wave writes its 64 x 64 block (scaled, bf16) into
@@ -568,7 +582,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
 #pragma unroll
     for (int qg = 0; qg < 4; ++qg) {
       const int rl = 16 * qg + l16;
-      const float inv = inv_l[rl];
+      const float inv = inv_l[qg];
 #pragma unroll
       for (int d = 0; d < kDbWave; ++d) {
         const f32x4 v = oacc[d][qg] * inv;
@@ -594,7 +608,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   for (int qg = 0; qg < 4; ++qg) {
     const int r = row0 + 16 * qg + l16;
     if (r >= nrows) continue;
-    const float inv = inv_l[16 * qg + l16];
+    const float inv = inv_l[qg];
     if (wk.nsplit == 1) {
       bf16* orp = p.o + b * p.o_sb + r * p.o_sh + col;
 #pragma unroll
