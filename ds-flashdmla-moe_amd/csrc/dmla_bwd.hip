@@ -15,7 +15,7 @@
 //   bwd_dkdv_kernel       per 64-key block, streaming 32-row tiles: S, P, dP and dS' = scale dS
 //                         on MFMA, dK_lat accumulated in registers (V fold included), dS'
 //                         written once to HBM as fp16 16x16 blocks;
-//   bwd_dq_kernel         dQ = dS' K_lat per 64-row tile over its causal key range;
+//   bwd_dq_kernel         dQ = dS' K_lat per 128-row tile over its causal key range;
 //   bwd_dk_reduce_kernel  sums the dK_lat partials of the row segments in a fixed order.
 // No atomics anywhere: the result is bitwise deterministic.
 //
@@ -46,9 +46,12 @@ constexpr int kCb = kDqk / 16;                      // 36 column blocks of dK / 
 constexpr int kPartFloats = kKeys * kDqk;           // one dK partial: 64 keys x 576 fp32
 constexpr int kMaxParts = 64;
 // dQ kernel: stage = dS' blocks of 64 rows x 32 keys (4 KB) + K^T of 576 dims x 32 keys (36 KB)
-constexpr int kDqDsBytes = 4096;
+constexpr int kDqRows = 128;                        // rows per dQ workgroup (8 waves, two row halves)
+constexpr int kDqThreads = 512;
+constexpr int kDqDsBytes = 8192;
 constexpr int kDqStageBytes = kDqDsBytes + kDqk * 64;
-constexpr int kDqLds = 2 * kDqStageBytes;           // 80 KB
+constexpr int kDqStages = 3;
+constexpr int kDqLds = kDqStages * kDqStageBytes;   // 132 KB
 static_assert(kDkdvLds <= 160 * 1024 && kDqLds <= 160 * 1024, "LDS budget");
 
 struct BwdParams {
@@ -81,15 +84,15 @@ struct BwdParams {
 
 // ---- work split of the dK/dV kernel, shared by the host and the reduction ------------------
 // Key block kb needs the row tiles from first_row_tile(kb) on (causal: rows whose position can
-// see key 64 kb), rounded down to an even tile so that every 64-row dQ tile that reads a dS'
-// block of kb finds it written.  Blocks kb and n_kb-1-kb form a pair: the first is walked from
+// see key 64 kb), rounded down to a multiple of four tiles so that every 128-row dQ tile that
+// reads a dS' block of kb finds it written.  Blocks kb and n_kb-1-kb form a pair: the first is walked from
 // the last row tile down, the second from its first row tile up, so every pair has about the
 // same length and, at any moment, all pairs of a batch element read the same one or two row
 // tiles (L2 sharing).  Each pair's steps are cut into `parts` equal segments.
 __host__ __device__ inline int first_row_tile(int causal, int Sq, int Sk, int H, int kb) {
   if (!causal) return 0;
   const int first_pos = max(0, kKeys * kb - (Sk - Sq));
-  return 2 * (int)(((int64_t)first_pos * H) / 64);
+  return 4 * (int)(((int64_t)first_pos * H) / 128);
 }
 struct PairPlan {
   int kb_a, kb_b, steps_a, total;
@@ -475,46 +478,61 @@ bwd_dkdv_kernel(BwdParams p) {
 }
 
 // ---- 4. dQ = dS' K_lat ----------------------------------------------------------------------
-// Workgroup = 4 waves on 64 rows x 576 dims; wave w owns column blocks w, w+4, .., w+32 of all
-// four row blocks (36 accumulators).  Per 32-key tile: dS' (A operand, row fixed per lane) from
-// the stored C-order blocks through ds_read_b64_tr_b16, K^T (B operand) with b128 reads.
-__global__ void __launch_bounds__(kBwdThreads, 1) bwd_dq_kernel(BwdParams p) {
+// Workgroup = 8 waves on 128 rows x 576 dims; wave w owns column blocks w%4, w%4+4, .., +32 of
+// the four row blocks of its row half w/4 (36 accumulators), so each 36 KB K^T tile staged in
+// LDS serves 128 rows.  Per 32-key tile: dS' (A operand, row fixed per lane) from the stored
+// C-order blocks through ds_read_b64_tr_b16, K^T (B operand) with b128 reads.  Tiles flow
+// through a 3-slot ring: the copies of tile kt+2 go out between the MFMAs of tile kt, so the
+// dS' blocks (read from HBM) have two tiles of time to land.
+__global__ void __launch_bounds__(kDqThreads, 1) bwd_dq_kernel(BwdParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[kDqLds];
   DMLA_LDS char* lds = (DMLA_LDS char*)smem;
   const int wave = uniform(threadIdx.x >> 6);
   const int lane = lane_id();
-  const int n_t = (p.R + 63) / 64;
+  const int n_t = (p.R + kDqRows - 1) / kDqRows;
   // Heaviest (latest) row tiles first.
   const int b = (int)blockIdx.x % p.B;
   const int t = n_t - 1 - (int)blockIdx.x / p.B;
-  const int row0 = 64 * t;
-  const int last_row = min(p.R, row0 + 64) - 1;
+  const int row0 = kDqRows * t;
+  const int last_row = min(p.R, row0 + kDqRows) - 1;
   const int kmax = p.causal ? min(p.Sk - 1, last_row / p.H + (p.Sk - p.Sq)) : p.Sk - 1;
   const int n_kt = kmax >= 0 ? kmax / 32 + 1 : 0;
   const int l16 = lane & 15, g = lane >> 4;
   const int e = l16 >> 2, qq = l16 & 3;
+  const int rh = wave >> 2, wc = wave & 3;   // row half (64 rows) and column phase of this wave
   const unsigned lds_base = lds_addr(lds);
+  // Row blocks of 16 that exist in the dS' buffer (rows padded to 64).
+  const int n_rb = 2 * p.n_rt;
 
-  // Copies.  dS': wave w moves row block 4t + w, key blocks 2 kt, 2 kt + 1 (1 KB contiguous).
-  // K^T: 16 dims x 32 keys per copy (1 KB), wave w copies dim blocks w, w+4, .. (9 copies);
+  // Copies.  dS': wave w moves row block 8 t + w, key blocks 2 kt, 2 kt + 1 (1 KB contiguous).
+  // K^T: 16 dims x 32 keys per copy (1 KB), wave w copies dim blocks w, w+8, .. (5 or 4 copies);
   // lane l -> dim 16 n + l/4, physical chunk l%4 = logical chunk (l%4) ^ (l/16).
   const unsigned kt_voff = (unsigned)(((lane >> 2) * p.kt_ld + 8 * ((lane & 3) ^ (lane >> 4))) * 2);
-  auto stage = [&](int kt, int st) {
+  // Every wave issues exactly kDqCopies copies per stage (so one vmcnt value waits for a stage):
+  // a row block past the buffer copies row block 0 instead (its rows are not stored), and
+  // waves 4-7 copy their dim block w + 24 a second time (same bytes to the same place).
+  const int rblk = 8 * t + wave < n_rb ? 8 * t + wave : 0;
+  auto copy = [&](int kt, int st, int m) {
     const unsigned dst = lds_base + st * kDqStageBytes;
-    const _Float16* dsrc = p.ds + ((((int64_t)b * 2 * p.n_rt + 4 * t + wave) * (4 * p.n_kb)) + 2 * kt) * 256;
-    dma16(dsrc, 16u * lane, dst + wave * 1024);
-#pragma unroll
-    for (int m = 0; m < 9; ++m) {
-      const int n = wave + 4 * m;
+    if (m == 0) {
+      const _Float16* dsrc = p.ds + ((((int64_t)b * 2 * p.n_rt + rblk) * (4 * p.n_kb)) + 2 * kt) * 256;
+      dma16(dsrc, 16u * lane, dst + wave * 1024);
+    } else {
+      const int n0 = wave + 8 * (m - 1);
+      const int n = n0 < kDqk / 16 ? n0 : n0 - 8;
       const _Float16* ksrc = p.kt + ((int64_t)b * kDqk + 16 * n) * p.kt_ld + 32 * kt;
       dma16(ksrc, kt_voff, dst + kDqDsBytes + n * 1024);
     }
   };
+  auto stage = [&](int kt, int st) {
+#pragma unroll
+    for (int m = 0; m < 6; ++m) copy(kt, st, m);
+  };
   // dS' A operand of row block rq, half h: lane 4e+q of group g reads C-order lane
   // 16 q + 8 (g & 1) + 4 h + e of key block g >> 1 (see the tr-read rule in dmla_common.h).
-  const int a_off = (g >> 1) * 512 + 8 * (16 * qq + 8 * (g & 1) + e);
-  // K^T B operand of column block wave + 4u: dim row 16 cb + l16, logical chunk g.
-  const int b_off = kDqDsBytes + wave * 1024 + l16 * 64 + 16 * (g ^ e);
+  const int a_off = 4 * rh * 1024 + (g >> 1) * 512 + 8 * (16 * qq + 8 * (g & 1) + e);
+  // K^T B operand of column block wc + 4u: dim row 16 cb + l16, logical chunk g.
+  const int b_off = kDqDsBytes + wc * 1024 + l16 * 64 + 16 * (g ^ e);
 
   f32x4 acc[4][9];
 #pragma unroll
@@ -523,11 +541,15 @@ __global__ void __launch_bounds__(kBwdThreads, 1) bwd_dq_kernel(BwdParams p) {
     for (int v = 0; v < 9; ++v) acc[a][v] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (n_kt > 0) stage(0, 0);
+  if (n_kt > 1) stage(1, 1);
+  int st = 0;
   for (int kt = 0; kt < n_kt; ++kt) {
-    const int st = kt & 1;
-    wait_vmem();
+    // stage kt has landed; stage kt+1 (six copies per wave) may still be in flight
+    if (kt + 1 < n_kt) __builtin_amdgcn_s_waitcnt(0x0f76);   // vmcnt(6)
+    else wait_vmem();
     __syncthreads();
-    if (kt + 1 < n_kt) stage(kt + 1, st ^ 1);
+    const bool more = kt + 2 < n_kt;
+    const int st2 = st == 0 ? 2 : st - 1;   // (kt + 2) % 3
     const DMLA_LDS char* sb = lds + st * kDqStageBytes;
     f16x8 a[4];
 #pragma unroll
@@ -542,21 +564,24 @@ __global__ void __launch_bounds__(kBwdThreads, 1) bwd_dq_kernel(BwdParams p) {
       const f16x8 kb = *reinterpret_cast<const DMLA_LDS f16x8*>(sb + b_off + v * 4096);
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) acc[rq][v] = mfma_f16(a[rq], kb, acc[rq][v]);
+      // copies of stage kt+2 into the slot step kt-1 read, between the MFMAs
+      if (more && v < 6) copy(kt + 2, st2, v);
     }
+    st = st == 2 ? 0 : st + 1;
   }
 
-  // acc[rq][v] holds dQ[row0 + 16 rq + 4 g + i][16 (wave + 4 v) + l16].
+  // acc[rq][v] holds dQ[row0 + 64 rh + 16 rq + 4 g + i][16 (wc + 4 v) + l16].
 #pragma unroll
   for (int rq = 0; rq < 4; ++rq) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = row0 + 16 * rq + 4 * g + i;
+      const int r = row0 + 64 * rh + 16 * rq + 4 * g + i;
       if (r >= p.R) continue;
       const int pos = fast_div(r, p.hdiv), h = r - pos * p.H;
       const int64_t base = b * p.dq_sb + h * p.dq_sh + pos * p.dq_ss + l16;
 #pragma unroll
       for (int v = 0; v < 9; ++v) {
-        const int col = 16 * (wave + 4 * v);
+        const int col = 16 * (wc + 4 * v);
         if (p.dq_fp32) static_cast<float*>(p.dq)[base + col] = acc[rq][v][i];
         else static_cast<bf16*>(p.dq)[base + col] = (bf16)acc[rq][v][i];
       }
@@ -711,9 +736,9 @@ extern "C" int dmla_bwd_cache_latent(const void* q, const void* k_lat, const voi
   hipLaunchKernelGGL(bwd_kt_kernel, dim3(kDqk / 64, (unsigned)pl.n_kb, (unsigned)B), dim3(256), 0, s, p);
   const int64_t grid_kv = 8 * ((pl.n_items + 7) / 8);
   hipLaunchKernelGGL(bwd_dkdv_kernel, dim3((unsigned)grid_kv), dim3(kBwdThreads), 0, s, p);
-  const int64_t grid_q = B * ((pl.R + 63) / 64);
+  const int64_t grid_q = B * ((pl.R + kDqRows - 1) / kDqRows);
   if (grid_q > 0x7fffffff) return fail(DMLA_ERR_UNSUPPORTED, "dmla_bwd_cache_latent: grid too large");
-  hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)grid_q), dim3(kBwdThreads), 0, s, p);
+  hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)grid_q), dim3(kDqThreads), 0, s, p);
   hipLaunchKernelGGL(bwd_dk_reduce_kernel, dim3(4, (unsigned)pl.n_kb, (unsigned)B), dim3(256), 0, s, p);
   return check_launch("dmla_bwd_cache_latent");
 }
