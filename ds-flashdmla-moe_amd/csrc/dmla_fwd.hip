@@ -107,7 +107,9 @@ struct MqaParams {
   int max_pages;
   int head_groups;     // ceil(H / 64)
   int n_ranges;        // R of the decode plan
-  const int32_t* plan; // decode plan (see decode_plan_kernel)
+  const int32_t* plan; // decode plan (see decode_plan_kernel); unused when plan_inline
+  int plan_inline;     // every workgroup builds the plan in LDS (B <= kInlinePlanB, R <= kInlinePlanR)
+  int32_t* plan_out;   // with plan_inline: workgroup 0 stores the plan here (the combine reads it)
   bf16* part_o;        // [slots, H, 512] normalised partial outputs, rounded to bf16
   float* part_lse;     // [slots, H]
 };
@@ -134,6 +136,22 @@ constexpr int kPlanHeader = 8;
 constexpr int kSegCost = 16;                          // measured: ~18 us per segment, ~1.1 us per tile
 constexpr int kMaxSegTiles = 2 * kMaxSegPages - 2;   // a segment's pages fit its page registers
 __host__ __device__ inline int64_t plan_ints(int64_t B, int64_t R) { return kPlanHeader + 4 * B + 2 + 2 * R + 1; }
+// Inline plan: the decode kernel builds the plan itself, in LDS past the pipeline's area, when
+// the batch and the range count fit (the common serving case); the standalone plan kernel and
+// its global round trips are then skipped.
+constexpr int kInlinePlanB = kThreads;   // one sequence per thread
+constexpr int kInlinePlanR = kThreads;
+struct InlinePlan {
+  int tp[kInlinePlanB + 1];    // tile prefix
+  int neb[kInlinePlanB + 1];   // nonempty sequences before b
+  int ns[kInlinePlanB];        // split count
+  int fr[kInlinePlanB];        // first range
+  int sb[kInlinePlanB + 1];    // first partial slot
+  int rs[kInlinePlanR + 1];    // range starts
+  int tmp[kWaves];             // scan scratch
+};
+constexpr int kDecodeLdsBytes = kLdsBytes + (int)sizeof(InlinePlan);
+static_assert(kDecodeLdsBytes <= 160 * 1024, "LDS budget (decode)");
 
 template <bool kDecode, int kHalf>
 __device__ __noinline__ void mqa_fwd_exact(const MqaParams* params, Work wk, DMLA_LDS char* lds, int wave, int lane);
@@ -655,9 +673,127 @@ __device__ __noinline__ void mqa_fwd_exact(const MqaParams* params, Work wk, DML
   mqa_fwd_body<kDecode, kHalf, true>(p, &p, wk, lds, wave, lane);
 }
 
+// Exclusive prefix of one value per thread over the workgroup; `total` gets the sum.
+__device__ __forceinline__ int wg_exclusive_scan(int v, DMLA_LDS int* tmp, int& total) {
+  const int lane = lane_id(), wave = uniform(threadIdx.x >> 6);
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) tmp[wave] = x;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int v2 = tmp[w];
+    before += w < wave ? v2 : 0;
+    tot += v2;
+  }
+  __syncthreads();   // tmp is free again
+  total = tot;
+  return before + x - v;
+}
+
+// The decode plan built by a workgroup in LDS: the arithmetic of decode_plan_kernel with one
+// sequence and one range per thread.  Workgroup 0 also stores it in the plan layout, where
+// the combine reads the split counts and bases.
+__device__ __forceinline__ void build_inline_plan(const MqaParams& p, DMLA_LDS InlinePlan* ip) {
+  const int tid = threadIdx.x;
+  const int B = p.B, R = p.n_ranges;
+  int nt = 0;
+  if (tid < B) nt = (min(max(p.seqlens[tid], 0), p.max_pages * kPage) + kTileN - 1) / kTileN;
+  int total, nonempty;
+  const int tpb = wg_exclusive_scan(nt, ip->tmp, total);
+  const int nb = wg_exclusive_scan(nt > 0 ? 1 : 0, ip->tmp, nonempty);
+  if (tid < B) {
+    ip->tp[tid] = tpb;
+    ip->neb[tid] = nb;
+  }
+  if (tid == 0) ip->tp[B] = total;
+  const int64_t weighted = (int64_t)total + (int64_t)kSegCost * nonempty;
+  const int W = (int)max<int64_t>(1, (weighted + R - 1) / R);
+  __syncthreads();
+  // Range starts: weighted position r W -> the sequence holding it -> its tile (or the
+  // sequence's first tile when among its virtual ones).
+  for (int rr = tid; rr <= R; rr += kThreads) {
+    int t = total;
+    if (rr < R && (int64_t)rr * W < weighted) {
+      const int64_t pos = (int64_t)rr * W;
+      int lo = 0, hi = B - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if ((int64_t)ip->tp[mid] + (int64_t)kSegCost * ip->neb[mid] <= pos) lo = mid; else hi = mid - 1;
+      }
+      const int64_t off = pos - ((int64_t)ip->tp[lo] + (int64_t)kSegCost * ip->neb[lo]);
+      t = ip->tp[lo] + (int)max<int64_t>(0, off - kSegCost);
+      t = min(t, ip->tp[lo + 1]);
+    }
+    ip->rs[rr] = t;
+  }
+  __syncthreads();
+  auto range_of = [&](int t) {   // the last range starting at or before tile t
+    int lo = 0, hi = R - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) / 2;
+      if (ip->rs[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+  };
+  int ns = 0, fr = 0;
+  if (tid < B) {
+    const int tb = ip->tp[tid], te = ip->tp[tid + 1];
+    if (te > tb) {
+      fr = range_of(tb);
+      ns = range_of(te - 1) - fr + 1;
+    }
+  }
+  int nsplits;
+  const int sbb = wg_exclusive_scan(ns, ip->tmp, nsplits);
+  if (tid < B) {
+    ip->ns[tid] = ns;
+    ip->fr[tid] = fr;
+    ip->sb[tid] = sbb;
+  }
+  if (tid == 0) ip->sb[B] = nsplits;
+  __syncthreads();
+  if (blockIdx.x == 0 && p.plan_out != nullptr) {
+    int32_t* plan = p.plan_out;
+    int32_t* tile_prefix = plan + kPlanHeader;
+    int32_t* split_base = tile_prefix + B + 1;
+    int32_t* num_splits = split_base + B + 1;
+    int32_t* first_range = num_splits + B;
+    int32_t* range_start = first_range + B;
+    int32_t* range_first_b = range_start + R + 1;
+    for (int i = tid; i <= B; i += kThreads) {
+      tile_prefix[i] = ip->tp[i];
+      split_base[i] = ip->sb[i];
+    }
+    for (int i = tid; i < B; i += kThreads) {
+      num_splits[i] = ip->ns[i];
+      first_range[i] = ip->fr[i];
+    }
+    for (int i = tid; i <= R; i += kThreads) range_start[i] = ip->rs[i];
+    for (int i = tid; i < R; i += kThreads) {
+      const int t = ip->rs[i];
+      int lo = 0, hi = B - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if (ip->tp[mid] <= t) lo = mid; else hi = mid - 1;
+      }
+      range_first_b[i] = lo;
+    }
+    if (tid == 0) {
+      plan[0] = B; plan[1] = R; plan[2] = W; plan[3] = total; plan[4] = nsplits; plan[5] = kSegCost;
+      plan[6] = plan[7] = 0;
+    }
+  }
+}
+
 template <bool kDecode>
 __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
-  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+  __shared__ __attribute__((aligned(1024))) char smem[kDecode ? kDecodeLdsBytes : kLdsBytes];
   DMLA_LDS char* lds = (DMLA_LDS char*)smem;
   const int lane = lane_id();
   const int wave = uniform(threadIdx.x >> 6);
@@ -686,6 +822,9 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
     const int id = blockIdx.x;
     const int k = (id / 8) % p.head_groups;
     const int r = (id / (8 * p.head_groups)) * 8 + id % 8;
+    const bool inl = p.plan_inline != 0;
+    DMLA_LDS InlinePlan* ip = reinterpret_cast<DMLA_LDS InlinePlan*>(lds + kLdsBytes);
+    if (inl) build_inline_plan(p, ip);   // every workgroup, before any early exit
     if (r >= p.n_ranges) return;
     const int32_t* plan = p.plan;
     const int32_t* tile_prefix = plan + kPlanHeader;
@@ -694,13 +833,26 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
     const int32_t* first_range = num_splits + p.B;
     const int32_t* range_start = first_range + p.B;
     const int32_t* range_first_b = range_start + p.n_ranges + 1;
-    const int t0 = range_start[r], t1 = range_start[r + 1];
+    auto tp_of = [&](int i) { return inl ? ip->tp[i] : tile_prefix[i]; };
+    const int t0 = inl ? ip->rs[r] : range_start[r];
+    const int t1 = inl ? ip->rs[r + 1] : range_start[r + 1];
     if (t0 >= t1) return;
+    int first_b;
+    if (inl) {
+      int lo = 0, hi = p.B - 1;   // the sequence holding tile t0
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if (ip->tp[mid] <= t0) lo = mid; else hi = mid - 1;
+      }
+      first_b = lo;
+    } else {
+      first_b = range_first_b[r];
+    }
     const MqaParams* params = (const MqaParams*)(__builtin_amdgcn_kernarg_segment_ptr());
-    for (int bseq = range_first_b[r]; bseq < p.B; ++bseq) {
-      const int tb = tile_prefix[bseq];
+    for (int bseq = first_b; bseq < p.B; ++bseq) {
+      const int tb = tp_of(bseq);
       if (tb >= t1) break;
-      const int seg0 = max(t0, tb), seg1 = min(t1, tile_prefix[bseq + 1]);
+      const int seg0 = max(t0, tb), seg1 = min(t1, tp_of(bseq + 1));
       if (seg0 >= seg1) continue;   // an empty sequence (its output comes from the combine)
       wk.b = bseq;
       wk.row0 = k * kRowsPerWG;
@@ -708,9 +860,9 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
       wk.tile_begin = seg0 - tb;
       wk.tile_end = seg1 - tb;
       wk.page_begin = wk.tile_begin / (kPage / kTileN);
-      wk.nsplit = num_splits[bseq];
-      wk.split = r - first_range[bseq];
-      wk.slot = split_base[bseq] + wk.split;
+      wk.nsplit = inl ? ip->ns[bseq] : num_splits[bseq];
+      wk.split = r - (inl ? ip->fr[bseq] : first_range[bseq]);
+      wk.slot = (inl ? ip->sb[bseq] : split_base[bseq]) + wk.split;
       if (((wave >> 1) & 1) == 0) mqa_fwd_body<kDecode, 0, false>(p, params, wk, lds, wave, lane);
       else mqa_fwd_body<kDecode, 1, false>(p, params, wk, lds, wave, lane);
       __syncthreads();   // every LDS read of this segment is done before the next one's copies
@@ -990,18 +1142,17 @@ static int decode_validate(const void* q, const void* kv_pool, const int32_t* bl
   return DMLA_OK;
 }
 
-extern "C" int dmla_decode_paged_planned(const void* q, const void* kv_pool, const int32_t* block_table,
-                                         const int32_t* cache_seqlens, void* o, float* lse, int64_t B,
-                                         int64_t H, int64_t d_qk, int64_t d_v, int64_t page_size,
-                                         int64_t num_pages, int64_t max_pages_per_seq, int64_t q_sb,
-                                         int64_t q_sh, int64_t kv_sp, int64_t kv_ss, int64_t bt_sb,
-                                         int64_t o_sb, int64_t o_sh, float softmax_scale, const int32_t* plan,
-                                         void* workspace, int64_t workspace_bytes, dmla_stream_t stream) {
-  clear_error();
-  if (!plan) return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: null plan");
-  int rc0 = decode_validate(q, kv_pool, block_table, cache_seqlens, o, B, H, d_qk, d_v, page_size, num_pages,
-                            max_pages_per_seq, q_sb, q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale);
-  if (rc0 != DMLA_OK || B == 0 || H == 0) return rc0;
+namespace dmla {
+namespace {
+
+// Launches the decode kernel and the combine on partial buffers of `part_bytes` bytes.  With
+// plan_out set, the decode kernel builds the plan itself and stores it there for the combine;
+// otherwise it reads `plan`.
+int decode_launch(const void* q, const void* kv_pool, const int32_t* block_table, const int32_t* cache_seqlens,
+                  void* o, float* lse, int64_t B, int64_t H, int64_t num_pages, int64_t max_pages_per_seq,
+                  int64_t q_sb, int64_t q_sh, int64_t kv_sp, int64_t kv_ss, int64_t bt_sb, int64_t o_sb,
+                  int64_t o_sh, float softmax_scale, const int32_t* plan, int32_t* plan_out, void* workspace,
+                  int64_t workspace_bytes, hipStream_t stream) {
   const int64_t slots = decode_slots(B, H, max_pages_per_seq);
   const int64_t need = slots * H * (int64_t)(kDv * 2 + 4);   // bf16 partial rows, then fp32 lse
   if (workspace == nullptr || workspace_bytes < need)
@@ -1026,17 +1177,19 @@ extern "C" int dmla_decode_paged_planned(const void* q, const void* kv_pool, con
   p.max_pages = (int)max_pages_per_seq;
   p.head_groups = (int)((H + kRowsPerWG - 1) / kRowsPerWG);
   p.n_ranges = (int)decode_ranges(B, H, max_pages_per_seq);
-  p.plan = plan;
+  p.plan = plan_out != nullptr ? nullptr : plan;
+  p.plan_inline = plan_out != nullptr ? 1 : 0;
+  p.plan_out = plan_out;
   p.part_o = static_cast<bf16*>(workspace);
   p.part_lse = reinterpret_cast<float*>(p.part_o + slots * H * kDv);
   const int64_t grid = ((int64_t)(p.n_ranges + 7) / 8) * 8 * p.head_groups;
   if (grid > 0x7fffffff) return fail(DMLA_ERR_UNSUPPORTED, "dmla_decode_paged: grid too large");
-  hipLaunchKernelGGL(mqa_fwd_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(mqa_fwd_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, stream, p);
   int rc = check_launch("dmla_decode_paged");
   if (rc != DMLA_OK) return rc;
   // Sequences with one split were written by the decode kernel; the others (and the empty
   // ones: zeros, lse -inf) come from the combine.
-  const int32_t* tile_prefix = plan + kPlanHeader;
+  const int32_t* tile_prefix = (plan_out != nullptr ? plan_out : plan) + kPlanHeader;
   CombineArgs c = {};
   c.part_o16 = p.part_o;
   c.part_lse = p.part_lse;
@@ -1049,7 +1202,28 @@ extern "C" int dmla_decode_paged_planned(const void* q, const void* kv_pool, con
   c.po_ss = H * kDv; c.po_sh = kDv;
   c.lse_ss = H; c.lse_sh = 1;
   c.o_sb = o_sb; c.o_sh = o_sh;
-  return launch_lse_combine(c, (hipStream_t)stream, "dmla_decode_paged(combine)");
+  return launch_lse_combine(c, stream, "dmla_decode_paged(combine)");
+}
+
+
+}  // namespace
+}  // namespace dmla
+
+extern "C" int dmla_decode_paged_planned(const void* q, const void* kv_pool, const int32_t* block_table,
+                                         const int32_t* cache_seqlens, void* o, float* lse, int64_t B,
+                                         int64_t H, int64_t d_qk, int64_t d_v, int64_t page_size,
+                                         int64_t num_pages, int64_t max_pages_per_seq, int64_t q_sb,
+                                         int64_t q_sh, int64_t kv_sp, int64_t kv_ss, int64_t bt_sb,
+                                         int64_t o_sb, int64_t o_sh, float softmax_scale, const int32_t* plan,
+                                         void* workspace, int64_t workspace_bytes, dmla_stream_t stream) {
+  clear_error();
+  if (!plan) return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: null plan");
+  int rc0 = decode_validate(q, kv_pool, block_table, cache_seqlens, o, B, H, d_qk, d_v, page_size, num_pages,
+                            max_pages_per_seq, q_sb, q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale);
+  if (rc0 != DMLA_OK || B == 0 || H == 0) return rc0;
+  return decode_launch(q, kv_pool, block_table, cache_seqlens, o, lse, B, H, num_pages, max_pages_per_seq, q_sb,
+                       q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale, plan, nullptr, workspace,
+                       workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" int dmla_decode_paged(const void* q, const void* kv_pool, const int32_t* block_table,
@@ -1069,10 +1243,17 @@ extern "C" int dmla_decode_paged(const void* q, const void* kv_pool, const int32
                 (long long)need, (long long)workspace_bytes);
   if (!aligned16(workspace)) return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: workspace must be 16-byte aligned");
   const int64_t pb = dmla_decode_plan_bytes(B, H, max_pages_per_seq);
-  int rc = dmla_decode_plan(cache_seqlens, B, H, max_pages_per_seq, static_cast<int32_t*>(workspace), pb, stream);
+  int32_t* plan = static_cast<int32_t*>(workspace);
+  void* parts = static_cast<char*>(workspace) + pb;
+  // Small batches (the serving case): the decode kernel builds the plan itself and stores it in
+  // the workspace; otherwise the plan kernel runs first.
+  if (B <= kInlinePlanB && decode_ranges(B, H, max_pages_per_seq) <= kInlinePlanR)
+    return decode_launch(q, kv_pool, block_table, cache_seqlens, o, lse, B, H, num_pages, max_pages_per_seq, q_sb,
+                         q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale, nullptr, plan, parts,
+                         workspace_bytes - pb, (hipStream_t)stream);
+  int rc = dmla_decode_plan(cache_seqlens, B, H, max_pages_per_seq, plan, pb, stream);
   if (rc != DMLA_OK) return rc;
-  return dmla_decode_paged_planned(q, kv_pool, block_table, cache_seqlens, o, lse, B, H, d_qk, d_v, page_size,
-                                   num_pages, max_pages_per_seq, q_sb, q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh,
-                                   softmax_scale, static_cast<const int32_t*>(workspace),
-                                   static_cast<char*>(workspace) + pb, workspace_bytes - pb, stream);
+  return decode_launch(q, kv_pool, block_table, cache_seqlens, o, lse, B, H, num_pages, max_pages_per_seq, q_sb,
+                       q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale, plan, nullptr, parts,
+                       workspace_bytes - pb, (hipStream_t)stream);
 }

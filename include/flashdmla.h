@@ -109,8 +109,10 @@ int dmla_fwd_onthefly(const void* q, const void* k, const void* v, const void* w
  * never dereferenced: the sequence's output and lse are set to NaN instead.
  * Supported: d_qk = 576, d_v = 512, page_size = 64.
  *
- * dmla_decode_paged computes a decode plan (dmla_decode_plan) at the head of the workspace,
- * then runs dmla_decode_paged_planned on the rest.  The workspace is always required.
+ * dmla_decode_paged leaves the decode plan (the layout of dmla_decode_plan) at the head of the
+ * workspace and keeps the split partials in the rest: for B <= 512 (and at most 512 ranges)
+ * the decode kernel builds the plan itself and stores it there, otherwise dmla_decode_plan
+ * runs first and dmla_decode_paged_planned follows.  The workspace is always required.
  */
 int64_t dmla_decode_workspace_bytes(int64_t B, int64_t H, int64_t d_v, int64_t max_pages_per_seq);
 int dmla_decode_paged(const void* q, const void* kv_pool, const int32_t* block_table,

@@ -150,3 +150,43 @@ def test_decode_with_a_shared_plan_is_bit_identical(gpu):
         a, la = ops.flash_dmla_decode_paged(qq.to(gpu), *args, return_lse=True)
         b, lb = ops.flash_dmla_decode_paged(qq.to(gpu), *args, return_lse=True, plan=plan)
         assert torch.equal(a, b) and torch.equal(la, lb)
+
+
+@pytest.mark.gpu
+def test_decode_inline_plan_stores_the_plan_kernels_plan(gpu):
+    """For batches up to 512 sequences dmla_decode_paged builds the plan inside the decode kernel
+    and stores it at the start of the workspace (where the combine reads it): that stored plan
+    must equal the standalone plan kernel's, entry for entry."""
+    from python import _lib
+    lens = [3000, 17, 0, 8000, 640, 1, 64, 4097]
+    q, pool, table, sl = _paged(lens, 128, seed=95)
+    qg, pg, tg, sg = q.to(gpu), pool.to(gpu), table.to(gpu), sl.to(gpu)
+    B, H, max_pages = len(lens), 128, table.shape[1]
+    ws_bytes = int(_lib.lib().dmla_decode_workspace_bytes(B, H, 512, max_pages))
+    plan_bytes = int(_lib.lib().dmla_decode_plan_bytes(B, H, max_pages))
+    ws = torch.full((ws_bytes,), 0x5A, dtype=torch.uint8, device=gpu)
+    o = torch.empty((B, H, 512), dtype=torch.bfloat16, device=gpu)
+    _lib.call("dmla_decode_paged", qg.data_ptr(), pg.data_ptr(), tg.data_ptr(), sg.data_ptr(), o.data_ptr(), None,
+              B, H, 576, 512, 64, pool.shape[0], max_pages, qg.stride(0), qg.stride(1), pg.stride(0), pg.stride(1),
+              tg.stride(0), o.stride(0), o.stride(1), SCALE, ws.data_ptr(), ws_bytes,
+              torch.cuda.current_stream().cuda_stream)
+    plan = ops.flash_dmla_decode_plan(sg, H, max_pages)
+    torch.cuda.synchronize()
+    ref = plan.cpu()
+    n = 8 + 4 * B + 2 + 2 * int(ref[1]) + 1   # header, per-sequence arrays, range arrays
+    stored = ws[:plan_bytes].view(torch.int32).cpu()[:n]
+    bad = (stored != ref[:n]).nonzero().flatten().tolist()
+    assert not bad, f"plan entries differ at {bad[:8]}: stored {stored[bad[:8]].tolist()} vs {ref[bad[:8]].tolist()}"
+
+
+@pytest.mark.gpu
+def test_decode_large_batch_uses_the_plan_kernel(gpu):
+    """600 short sequences: past the inline-plan limit, the plan kernel runs first."""
+    g = torch.Generator().manual_seed(97)
+    lens = torch.randint(0, 96, (600,), generator=g).tolist()
+    q, pool, table, sl = _paged(lens, 16, seed=98)
+    o, lse = ops.flash_dmla_decode_paged(q.to(gpu), pool.to(gpu), table.to(gpu), sl.to(gpu), 512, SCALE,
+                                         return_lse=True)
+    o_ref, lse_ref = R.dmla_decode_paged(q.float(), pool.float(), table, sl, 512, SCALE)
+    assert_out_close(o, o_ref)
+    _lse_close(lse, lse_ref)   # empty sequences: lse -inf on both sides
