@@ -267,21 +267,28 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
       }
     }
     // P = exp2(s scale - mref) (0 for masked keys and for rows without a finite reference yet).
+    // The row sums add the fp16 P that the PV product multiplies, two per v_dot2c_f32_f16 (fp32
+    // accumulation): half the instructions of one fp32 add per score.
     f16x8 pa[4][2];   // A operand of O += P V_lat: [rb][ks], keys of k-step ks in V_lat^T order
+    const f16x2 ones = {(_Float16)1.f, (_Float16)1.f};
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       const float nmr = mref[rb] == kNegInf ? 0.f : -mref[rb];
-      float ps = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float e = fast_exp2(__builtin_fmaf(s[kb][rb][i], sl2, nmr));
-          ps += e;
           pa[rb][kb >> 1][4 * (kb & 1) + i] = (_Float16)e;
         }
       }
-      lsum[rb] += ps;
+      float ps = lsum[rb];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          ps = __builtin_amdgcn_fdot2(f16x2{pa[rb][ks][2 * j], pa[rb][ks][2 * j + 1]}, ones, ps, false);
+      lsum[rb] = ps;
     }
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
