@@ -15,6 +15,8 @@
 // K_lat, V_lat, Q and P enter the attention products as fp16 (Q converted exactly, the rest
 // rounded from fp32): 3 more significand bits than bf16, which keeps the rounding of the
 // latent tiles well inside the output tolerance even for rows that see only a few keys.
+// K_lat is stored multiplied by scale log2(e) and the score accumulators start at -m_ref, so
+// the MFMA hands the softmax its exp2 arguments directly.
 // Every MFMA operand read from LDS is a conflict-free 16-byte read: K_lat rows for S^T and a
 // V_lat^T tile whose key order matches the C layout of S^T (so P needs no transposition).
 //
@@ -165,6 +167,9 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
           if constexpr (kK) c = mfma_bf16(wreg[ks], x, c);   // K_lat^T[dim 16 pdb + 4g + i][key 16 kb + l16]
           else c = mfma_bf16(x, wreg[ks], c);                // V_lat[key 16 kb + 4g + i][dim 16 pdb + l16]
         }
+        // K_lat is stored pre-multiplied by scale log2(e), so that scores come out of the MFMA in
+        // log2 units (one fp16 rounding either way).
+        if constexpr (kK) c *= p.scale_log2;
         f16x4 v;
         v[0] = (_Float16)c[0]; v[1] = (_Float16)c[1]; v[2] = (_Float16)c[2]; v[3] = (_Float16)c[3];
         if constexpr (kK) {
@@ -195,7 +200,6 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
     mtrue[rb] = kNegInf;
     lsum[rb] = 0.f;
   }
-  const float sl2 = p.scale_log2;
   const int own_pos0 = row0 + l16;   // position of own row 16 rb + l16 is own_pos0 + 16 rb
 
   if (n_t > 0) project(0, 0);
@@ -209,7 +213,12 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
 
     const DMLA_LDS char* klat = lds + kLatOff + ((t & 1) * 2) * kLatBytes;
     const DMLA_LDS char* vlat = klat + kLatBytes;
-    // S^T[kb][rb]: keys 16 kb + 4g + i, row 16 rb + l16
+    // x[kb][rb] = S^T in log2 units minus the row's reference: keys 16 kb + 4g + i, row 16 rb +
+    // l16.  The MFMA accumulators start at -m_ref (0 while a row has no reference), so x is the
+    // exp2 argument as it leaves the matrix core.
+    float nmr[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) nmr[rb] = mref[rb] == kNegInf ? 0.f : -mref[rb];
     f32x4 s[4][4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
@@ -217,13 +226,11 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
       const f16x8 k1 = *reinterpret_cast<const DMLA_LDS f16x8*>(klat + lat_off(16 * kb + l16, 4 + g));
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb) {
-        s[kb][rb] = mfma_f16(k0, qreg[rb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+        s[kb][rb] = mfma_f16(k0, qreg[rb][0], f32x4{nmr[rb], nmr[rb], nmr[rb], nmr[rb]});
         s[kb][rb] = mfma_f16(k1, qreg[rb][1], s[kb][rb]);
       }
     }
-    // Scores stay unscaled (scale > 0 keeps their order): the tile max is taken on them and the
-    // scale folds into the exp2 argument.  Only tiles that reach past some row's limit or past
-    // Sk are masked, in a block of their own.
+    // Only tiles that reach past some row's limit or past Sk are masked, in a block of their own.
     const int key0 = t * kOtfKeys;
     if (key0 + kOtfKeys > p.Sk || (p.causal && key0 + kOtfKeys - 1 > row0 + off)) {
 #pragma unroll
@@ -244,7 +251,7 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
         mx = fmaxf(mx, fmaxf(fmaxf(s[kb][rb][0], s[kb][rb][1]), fmaxf(s[kb][rb][2], s[kb][rb][3])));
-      mx *= sl2;
+      mx -= nmr[rb];   // the tile's max score in log2 units
       mtrue[rb] = fmaxf(mtrue[rb], mx);
       raise |= mx > mref[rb] + kSlack;
     }
@@ -257,6 +264,10 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
         const float f = mnew == kNegInf ? 1.f : fast_exp2(mref[rb] - mnew);   // 0 when mref = -inf
         lsum[rb] *= f;
         mref[rb] = mnew;
+        // this tile's arguments move to the new reference
+        const float dn = (mnew == kNegInf ? 0.f : -mnew) - nmr[rb];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) s[kb][rb] += dn;
         // O rows 16 rb + 4 g + i are own rows of lanes with l16 = 4 g + i.
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -273,12 +284,11 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
     const f16x2 ones = {(_Float16)1.f, (_Float16)1.f};
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
-      const float nmr = mref[rb] == kNegInf ? 0.f : -mref[rb];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float e = fast_exp2(__builtin_fmaf(s[kb][rb][i], sl2, nmr));
+          const float e = fast_exp2(s[kb][rb][i]);
           pa[rb][kb >> 1][4 * (kb & 1) + i] = (_Float16)e;
         }
       }
