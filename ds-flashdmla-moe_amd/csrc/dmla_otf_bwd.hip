@@ -200,8 +200,11 @@ __global__ void __launch_bounds__(256) otf_bwd_proj_kernel(OtfBwdParams p) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) c = mfma_bf16(wa[db][ks], cur[ks], c);   // X_lat^T[dim 16 db + 4 g + i][key]
       f16x4 o;
+      // K_lat is stored multiplied by scale log2(e): S then comes out in log2 units and the
+      // score accumulators can start at -lse2 (dQ takes ln 2 instead of the scale).
+      const float mul = x ? 1.f : p.scale_log2;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = key < p.Sk ? (_Float16)c[i] : (_Float16)0.f;
+      for (int i = 0; i < 4; ++i) o[i] = key < p.Sk ? (_Float16)(c[i] * mul) : (_Float16)0.f;
       *reinterpret_cast<f16x4*>(dst + (size_t)key * kLat + 16 * db + 4 * g) = o;
     }
   }
@@ -212,7 +215,8 @@ __global__ void __launch_bounds__(256) otf_bwd_proj_kernel(OtfBwdParams p) {
 // Rows stream in stages of 64 (Q and dO as fp16, copied global -> LDS one stage ahead), from
 // the first row that sees any of the block's keys.  Per 32-row sub-tile and wave:
 //   S  = Q K_lat^T, dP = dO V_lat^T    (A = Q / dO rows from LDS, B = K_lat / V_lat in registers)
-//   P  = exp2(S scale log2e - lse2), dS = P (dP - D)
+//   P  = exp2(S scale log2e - lse2), dS = P (dP - D)   (K_lat stored times scale log2e; the S
+//        accumulators start at -lse2, so the product is the exp2 argument)
 //   dV_lat^T += dO^T P, dK_lat^T += Q^T dS   (A = dO^T / Q^T by transposed reads; B = P / dS
 //                                           straight from the C tiles of S and dP)
 // Grid: key blocks heavy first (block 0 sees every row under the causal mask).
@@ -251,7 +255,6 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
   const float* lse2 = p.lse2 + (size_t)bh * p.Sqp;
   const float* nd = p.nd + (size_t)bh * p.Sqp;
   const unsigned lbase = lds_addr(lds);
-  const float sl2 = p.scale_log2;
 
   // One 32-row sub-tile; kMask applies the causal / key-range mask (only sub-tiles that reach
   // past some pair's limit need it), so the common case is straight-line code.
@@ -268,7 +271,7 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
       const f16x8 oa1 = lds_f16x8(dt + row_operand_off(lane, rb, 1));
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        sacc[rb][kb] = mfma_f16(qa0, kreg[kb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+        sacc[rb][kb] = mfma_f16(qa0, kreg[kb][0], -ls[rb]);   // S log2(e) scale - lse2
         sacc[rb][kb] = mfma_f16(qa1, kreg[kb][1], sacc[rb][kb]);
         dpacc[rb][kb] = mfma_f16(oa0, vreg[kb][0], ndv[rb]);
         dpacc[rb][kb] = mfma_f16(oa1, vreg[kb][1], dpacc[rb][kb]);
@@ -281,7 +284,7 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float pv = fast_exp2(__builtin_fmaf(sacc[rb][kb][i], sl2, -ls[rb][i]));
+          float pv = fast_exp2(sacc[rb][kb][i]);
           if constexpr (kMask) {
             const int row = r0 + 16 * rb + 4 * g + i, key = k0 + 16 * kb + l16;
             const int lim = p.causal ? min(row + off, p.Sk - 1) : p.Sk - 1;
@@ -400,7 +403,6 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
   const _Float16* ksrc = p.klat + (size_t)bh * p.Skp * kLat;
   const _Float16* vsrc = p.vlat + (size_t)bh * p.Skp * kLat;
   const unsigned lbase = lds_addr(lds);
-  const float sl2 = p.scale_log2;
 
   auto subtile = [&](const DMLA_LDS char* kt, const DMLA_LDS char* vt, int c0, auto mask_tag) {
     constexpr bool kMask = decltype(mask_tag)::value;
@@ -413,7 +415,7 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
       const f16x8 va1 = lds_f16x8(vt + row_operand_off(lane, kb, 1));
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        sT[kb][rb] = mfma_f16(ka0, qreg[rb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+        sT[kb][rb] = mfma_f16(ka0, qreg[rb][0], f32x4{-lse[rb], -lse[rb], -lse[rb], -lse[rb]});
         sT[kb][rb] = mfma_f16(ka1, qreg[rb][1], sT[kb][rb]);
         dpT[kb][rb] = mfma_f16(va0, oreg[rb][0], ndv[rb]);
         dpT[kb][rb] = mfma_f16(va1, oreg[rb][1], dpT[kb][rb]);
@@ -426,7 +428,7 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float pv = fast_exp2(__builtin_fmaf(sT[kb][rb][i], sl2, -lse[rb]));
+          float pv = fast_exp2(sT[kb][rb][i]);
           if constexpr (kMask) {
             const int row = r0 + 16 * rb + l16, key = c0 + 16 * kb + 4 * g + i;
             const int lim = p.causal ? min(row + off, p.Sk - 1) : p.Sk - 1;
@@ -472,7 +474,7 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
       if (row >= p.Sq) continue;
       bf16* out = p.dq + b * p.dq_sb + h * p.dq_sh + (int64_t)row * p.dq_ss + l16;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) out[16 * db] = (bf16)(dq[rb][db][i] * p.scale);
+      for (int db = 0; db < 4; ++db) out[16 * db] = (bf16)(dq[rb][db][i] * kLn2);   // scale / (scale log2 e)
     }
 }
 
