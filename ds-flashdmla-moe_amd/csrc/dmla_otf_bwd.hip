@@ -164,7 +164,9 @@ __global__ void __launch_bounds__(256) otf_bwd_wt_kernel(OtfBwdParams p) {
 // 0-1 project K, waves 2-3 V, each taking every other 16-key block with the next block's rows
 // loaded while the current one is multiplied.  Grid (Skp / 256 rounded up, H, B).
 __global__ void __launch_bounds__(256) otf_bwd_proj_kernel(OtfBwdParams p) {
-  const int h = blockIdx.y, b = blockIdx.z, bh = b * p.H + h;
+  // Heads fastest in the grid: workgroups issued together read neighbouring 256-byte pieces of
+  // the same [B, S, H, 128] rows (the 16 key blocks of one head lie 8 KB apart per key).
+  const int h = blockIdx.x, b = blockIdx.z, bh = b * p.H + h;
   const int wave = uniform(threadIdx.x >> 6), lane = lane_id(), l16 = lane & 15, g = lane >> 4;
   const int x = wave >> 1;
   bf16x8 wa[4][4];   // [db][ks]: W^T row 16 db + l16, input dims 32 ks + 8 g ..
@@ -178,7 +180,7 @@ __global__ void __launch_bounds__(256) otf_bwd_proj_kernel(OtfBwdParams p) {
   const bf16* src = x ? p.v + b * p.v_sb + h * p.v_sh : p.k + b * p.k_sb + h * p.k_sh;
   const int64_t ss = x ? p.v_ss : p.k_ss;
   _Float16* dst = (x ? p.vlat : p.klat) + (size_t)bh * p.Skp * kLat;
-  const int key_base = blockIdx.x * 256;
+  const int key_base = blockIdx.y * 256;
   const int n_kb = min(16, (p.Skp - key_base) / 16);
   bf16x8 xr[4];
   auto load = [&](int kb) {
@@ -695,7 +697,7 @@ extern "C" int dmla_bwd_onthefly(const void* q, const void* k, const void* v, co
                 (long long)pl.bytes, (long long)workspace_bytes);
   if (!aligned16(workspace)) return fail(DMLA_ERR_INVALID_ARG, "dmla_bwd_onthefly: workspace must be 16-byte aligned");
   const int64_t grid_kv = B * H * (pl.Skp / kKeyBlk), grid_q = B * H * (pl.Sqp / kRowBlk);
-  if (grid_kv > 0x7fffffff || grid_q > 0x7fffffff || B * H > 65535 || 2 * B > 65535)
+  if (grid_kv > 0x7fffffff || grid_q > 0x7fffffff || B * H > 65535 || 2 * B > 65535 || (pl.Skp + 255) / 256 > 65535)
     return fail(DMLA_ERR_UNSUPPORTED, "dmla_bwd_onthefly: grid too large");
 
   OtfBwdParams p = {};
@@ -743,7 +745,7 @@ extern "C" int dmla_bwd_onthefly(const void* q, const void* k, const void* v, co
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(otf_bwd_prep_kernel, dim3((unsigned)(pl.Sqp / 32), (unsigned)(B * H)), dim3(256), 0, s, p);
   hipLaunchKernelGGL(otf_bwd_wt_kernel, dim3((unsigned)H, 2), dim3(256), 0, s, p);
-  hipLaunchKernelGGL(otf_bwd_proj_kernel, dim3((unsigned)((pl.Skp + 255) / 256), (unsigned)H, (unsigned)B), dim3(256),
+  hipLaunchKernelGGL(otf_bwd_proj_kernel, dim3((unsigned)H, (unsigned)((pl.Skp + 255) / 256), (unsigned)B), dim3(256),
                      0, s, p);
   hipLaunchKernelGGL(otf_bwd_dkdv_kernel, dim3((unsigned)grid_kv), dim3(256), 0, s, p);
   hipLaunchKernelGGL(otf_bwd_dq_kernel, dim3((unsigned)grid_q), dim3(256), 0, s, p);
