@@ -3,7 +3,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--secondary decode,bwd,onthefly] [--no-cpu-baseline]
 
-Primary line (BASELINE.json metric, config 2): cache-latent DMLA prefill forward, bf16, causal,
+Primary line (headline metric, config 2): cache-latent DMLA prefill forward, bf16, causal,
 B=4, H=16, S=2048, Q [B,H,S,576], shared K_lat [B,S,576], V_lat = K_lat[..., :512], scale
 1/sqrt(192), inputs N(0,1)*0.5 (synthetic, seeded).  One step = one forward launch over the
 whole batch with inputs resident in HBM.  value = algorithmic TFLOP/s over the K timed steps,
@@ -98,7 +98,7 @@ def bench_prefill(steps, warmup, cpu_baseline):
         "value": flops / (wall_ms * 1e-3) / 1e12,
         "unit": "TFLOP/s",
         "ms_per_step": wall_ms,
-        "config": {"workload": "cache-latent prefill fwd (BASELINE config 2)", "batch": B, "heads": H,
+        "config": {"workload": "cache-latent prefill fwd (benchmark config 2)", "batch": B, "heads": H,
                    "seq_len": S, "d_qk": 576, "d_v": 512, "causal": True, "softmax_scale": SCALE},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": _load_traffic("prefill"),
@@ -190,7 +190,7 @@ def bench_decode(steps, warmup, cpu_baseline):
         "value": bytes_total / (wall_ms * 1e-3) / 1e9,
         "unit": "GB/s",
         "ms_per_step": wall_ms,
-        "config": {"workload": "paged decode (BASELINE config 3)", "batch": B, "heads": H, "page": P,
+        "config": {"workload": "paged decode (benchmark config 3)", "batch": B, "heads": H, "page": P,
                    "ctx_sum": int(lens.sum()), "ctx_min": int(lens.min()), "ctx_max": int(lens.max())},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": _load_traffic("decode"),
@@ -248,7 +248,7 @@ def bench_onthefly(steps, warmup, cpu_baseline):
         "value": flops / (wall_ms * 1e-3) / 1e12,
         "unit": "TFLOP/s",
         "ms_per_step": wall_ms,
-        "config": {"workload": "on-the-fly prefill fwd (BASELINE config 4)", "batch": B, "heads": H, "seq_len": S,
+        "config": {"workload": "on-the-fly prefill fwd (benchmark config 4)", "batch": B, "heads": H, "seq_len": S,
                    "d_in": 128, "d_lat": 64, "causal": True, "softmax_scale": 0.125},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": _load_traffic("onthefly"),
@@ -297,7 +297,7 @@ def bench_bwd(steps, warmup, cpu_baseline):
         "value": flops / (wall_ms * 1e-3) / 1e12,
         "unit": "TFLOP/s",
         "ms_per_step": wall_ms,
-        "config": {"workload": "cache-latent backward (BASELINE config 5)", "batch": B, "heads": H, "seq_len": S,
+        "config": {"workload": "cache-latent backward (benchmark config 5)", "batch": B, "heads": H, "seq_len": S,
                    "d_qk": 576, "d_v": 512, "causal": True, "softmax_scale": SCALE},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": _load_traffic("bwd"),
@@ -355,7 +355,7 @@ def bench_onthefly_bwd(steps, warmup, cpu_baseline):
         "value": flops / (wall_ms * 1e-3) / 1e12,
         "unit": "TFLOP/s",
         "ms_per_step": wall_ms,
-        "config": {"workload": "on-the-fly backward at the BASELINE config 4 shapes", "batch": B, "heads": H,
+        "config": {"workload": "on-the-fly backward at the benchmark config 4 shapes", "batch": B, "heads": H,
                    "seq_len": S, "d_in": 128, "d_lat": 64, "causal": True, "softmax_scale": 0.125},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": _load_traffic("onthefly_bwd"),
@@ -414,8 +414,8 @@ def main():
                     help="only run MIB-sized device copies (HBM counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs and reports the "
-              "single-GPU path, see DESIGN.md for how it would shard", file=sys.stderr)
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): every box here has a single GPU, "
+              "so this build runs and reports the single-GPU path", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -452,7 +452,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1)*0.5 inputs of the BASELINE config 2 shapes)",
+        "data": "synthetic (seeded N(0,1)*0.5 inputs of the benchmark config 2 shapes)",
         "config": primary["config"],
         "roofline": primary["roofline"],
         "cpu_baseline": primary.get("cpu_baseline"),

@@ -3,7 +3,7 @@
 //     dmla_decode_paged reads through the block table);
 //   * the split-KV log-sum-exp combine, also usable on its own (e.g. to merge partials that
 //     several devices computed over disjoint page ranges of one context).
-// Neither has a reference counterpart: the reference has no paged decode.
+// Neither has a reference counterpart: the reference has no paged decode (benchmark config 3).
 #include <type_traits>
 
 #include "dmla_common.h"

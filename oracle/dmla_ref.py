@@ -23,7 +23,7 @@ whose math this module restates in PyTorch eager (fp32 by default, fp64 for pinn
   * the same backward in the on-the-fly mode, through the projections K WK, V WV to the
     gradients of K, V, WK and WV (README.md:14 makes WK / WV learnable)
                                                                         -> dmla_bwd_onthefly
-  * paged decode (no reference counterpart): contiguous attention over the
+  * paged decode (no reference counterpart; benchmark config 3): contiguous attention over the
     tokens gathered through the block table                           -> dmla_decode_paged
   * the paged-cache append that produces those pages and the split-KV LSE combine (no
     reference counterparts)                                           -> kv_append, lse_combine

@@ -1,4 +1,4 @@
-"""Writes the golden fixture of BASELINE config 1 (tiny cache-latent DMLA forward, fp32).
+"""Writes the golden fixture of benchmark config 1 (tiny cache-latent DMLA forward, fp32).
 
 Config 1: B=1, H=4, S=128, causal; Q [1,4,128,64] and a shared K_lat [1,128,64], all N(0,1)
 from torch.Generator().manual_seed(0); V_lat = K_lat[..., :32]; softmax scale 1/sqrt(64).

@@ -101,7 +101,7 @@ def test_bwd_strided_views_and_fp32_outputs(gpu):
 
 @pytest.mark.gpu
 def test_bwd_config5_full_shape(gpu):
-    # B=4, H=16, S=2048, causal, dO ~ N(0, 1); references in fp32 on the GPU.
+    # benchmark config 5: B=4, H=16, S=2048, causal, dO ~ N(0, 1); references in fp32 on the GPU.
     q, k, do = _inputs(4, 16, 2048, 2048, seed=0)
     _check(gpu, q, k, do, True, ref_device="gpu")
 

@@ -91,7 +91,7 @@ def test_decode_bad_page_index_gives_nan_not_a_fault(gpu):
 
 @pytest.mark.gpu
 def test_decode_config3_full_shape(gpu):
-    # B=64, H=128, contexts uniform in [1024, 8192], 64-token pages in a
+    # benchmark config 3: B=64, H=128, contexts uniform in [1024, 8192], 64-token pages in a
     # seeded random permutation.
     g = torch.Generator().manual_seed(3)
     lens = torch.randint(1024, 8193, (64,), generator=g).tolist()

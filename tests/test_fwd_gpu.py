@@ -2,7 +2,7 @@
 
 Inputs are generated on the CPU from seeded generators and cast to bf16; the oracle consumes
 the bf16->fp32 upcasts, so both sides see bit-identical data.  Small cases run the oracle on
-the CPU; the full BASELINE config 2 shape runs the same oracle code on the GPU in fp32.
+the CPU; the full benchmark config 2 shape runs the same oracle code on the GPU in fp32.
 """
 import math
 
@@ -93,7 +93,7 @@ def test_fwd_score_jump_in_the_last_tile(gpu):
 
 @pytest.mark.gpu
 def test_fwd_config2_full_shape(gpu):
-    # B=4, H=16, S=2048, 576/512, N(0,1)*0.5, scale 1/sqrt(192), causal.
+    # benchmark config 2: B=4, H=16, S=2048, 576/512, N(0,1)*0.5, scale 1/sqrt(192), causal.
     q, k = _inputs(4, 16, 2048, 2048, seed=2)
     _check(gpu, q, k, True, oracle_device="gpu")
 

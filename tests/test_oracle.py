@@ -385,7 +385,7 @@ def test_decode_plan_covers_every_tile_once(lens, nr):
 
 
 def test_decode_plan_balances_tiles_plus_segment_costs():
-    # BASELINE config 3 shape: 64 contexts in [1024, 8192], 128 ranges
+    # benchmark config 3 shape: 64 contexts in [1024, 8192], 128 ranges
     g = torch.Generator().manual_seed(3)
     lens = torch.randint(1024, 8193, (64,), generator=g).tolist()
     plan = R.decode_plan(lens, 128, 128)

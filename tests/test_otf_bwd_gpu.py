@@ -12,7 +12,7 @@ rounding alone moves dwk by up to ~3e-2 at these sizes (the exact math fed with 
 bf16-rounded O, in fp64, against the exact gradient).  So against autograd each gradient may
 differ by that same-O error of the oracle plus 2e-2 max-abs, and by 1e-2 mean-rel.  dwk and dwv
 are compared in fp32, the op's default output type: they sum over every batch element and
-position and reach ~30 at config-4 sizes, where a bf16 rounding alone is 0.06.  Inputs follow BASELINE config 4:
+position and reach ~30 at config-4 sizes, where a bf16 rounding alone is 0.06.  Inputs follow benchmark config 4:
 q, k, v ~ N(0, 1), Xavier-uniform weights, scale 1/8, dO ~ N(0, 1).
 """
 import math
@@ -109,7 +109,7 @@ def test_otf_bwd_single_token(gpu):
 
 @pytest.mark.gpu
 def test_otf_bwd_config4_shape(gpu):
-    """BASELINE config 4 at full size (B=2, H=32, S=4096), oracle on the GPU in fp32."""
+    """benchmark config 4 at full size (B=2, H=32, S=4096), oracle on the GPU in fp32."""
     _check(gpu, 2, 32, 4096, 4096, True, seed=4, ref_device="gpu", autograd=False)
 
 

@@ -2,7 +2,7 @@
 
 The oracle projects K_lat = K WK and V_lat = V WV in fp32 and runs exact attention; the kernel
 projects on MFMA and rounds K_lat / V_lat (and P) to fp16 before the attention products, which
-the north-star tolerance (max-abs 2e-2, mean-rel 1e-2) covers.  Inputs follow BASELINE config 4:
+the north-star tolerance (max-abs 2e-2, mean-rel 1e-2) covers.  Inputs follow benchmark config 4:
 q, k, v ~ N(0, 1), wk and wv Xavier-uniform (bound sqrt(6 / (128 + 64))), scale 1/8.
 """
 import math
@@ -75,7 +75,7 @@ def test_otf_score_growth_moves_the_reference(gpu):
 
 @pytest.mark.gpu
 def test_otf_config4_full_shape(gpu):
-    # B=2, H=32, S=4096, causal; the oracle runs in fp32 on the GPU.
+    # benchmark config 4: B=2, H=32, S=4096, causal; the oracle runs in fp32 on the GPU.
     _check(gpu, 2, 32, 4096, 4096, True, seed=0, ref_device="gpu")
 
 
