@@ -180,6 +180,21 @@ def test_decode_inline_plan_stores_the_plan_kernels_plan(gpu):
 
 
 @pytest.mark.gpu
+def test_decode_inline_plan_at_its_batch_limit(gpu):
+    """512 sequences, the largest batch whose plan the decode kernel builds itself (one sequence
+    per thread of the workgroup, the last one included)."""
+    g = torch.Generator().manual_seed(99)
+    lens = torch.randint(0, 80, (512,), generator=g).tolist()
+    lens[-1] = 200   # the last thread's sequence spans several tiles
+    q, pool, table, sl = _paged(lens, 16, seed=100)
+    o, lse = ops.flash_dmla_decode_paged(q.to(gpu), pool.to(gpu), table.to(gpu), sl.to(gpu), 512, SCALE,
+                                         return_lse=True)
+    o_ref, lse_ref = R.dmla_decode_paged(q.float(), pool.float(), table, sl, 512, SCALE)
+    assert_out_close(o, o_ref)
+    _lse_close(lse, lse_ref)
+
+
+@pytest.mark.gpu
 def test_decode_large_batch_uses_the_plan_kernel(gpu):
     """600 short sequences: past the inline-plan limit, the plan kernel runs first."""
     g = torch.Generator().manual_seed(97)
