@@ -53,11 +53,12 @@ def _load_traffic(name):
 
 
 def _time_launches(fn, steps, warmup):
-    """Runs fn() warmup times, then `steps` timed times.  Returns (wall ms/step, kernel ms/launch).
+    """Runs fn() warmup times, then `steps` timed times.  Returns (wall ms/step, kernel stats).
 
     Wall time is bracketed by torch.cuda.synchronize() on both sides; per-launch durations
-    come from HIP events recorded on the current stream, which is the stream the C ABI
-    receives and launches on.
+    come from HIP events recorded around each launch on the current stream, which is the
+    stream the C ABI receives and launches on.  The kernel figure is the median launch (the
+    first launches of a short run can still see the clock ramp); the mean is reported beside it.
     """
     import torch
 
@@ -73,8 +74,20 @@ def _time_launches(fn, steps, warmup):
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    kern_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
-    return wall_ms, kern_ms
+    per = sorted(a.elapsed_time(b) for a, b in ev)
+    mid = len(per) // 2
+    median = per[mid] if len(per) % 2 else 0.5 * (per[mid - 1] + per[mid])
+    return wall_ms, {"median": median, "mean": sum(per) / len(per), "min": per[0], "max": per[-1],
+                     "launches": len(per)}
+
+
+def _roofline(bound, work, stats, peak, unit, traffic, kernel, work_key):
+    """roofline object from the median launch; the mean and spread ride along."""
+    achieved = work / (stats["median"] * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+    return {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit, "frac": achieved / peak,
+            "traffic": traffic, "kernel": kernel, "kernel_ms": stats["median"], "kernel_ms_mean": stats["mean"],
+            "kernel_ms_min": stats["min"], "kernel_ms_max": stats["max"], "launches_timed": stats["launches"],
+            work_key: work}
 
 
 def bench_prefill(steps, warmup, cpu_baseline):
@@ -91,8 +104,7 @@ def bench_prefill(steps, warmup, cpu_baseline):
     def step(i=0):
         ops.flash_dmla_fwd(q, k, 512, SCALE, True)
 
-    wall_ms, kern_ms = _time_launches(step, steps, warmup)
-    achieved = flops / (kern_ms * 1e-3) / 1e12
+    wall_ms, ks = _time_launches(step, steps, warmup)
     res = {
         "metric": "DMLA prefill TFLOP/s (cache-latent fwd, config 2)",
         "value": flops / (wall_ms * 1e-3) / 1e12,
@@ -100,10 +112,8 @@ def bench_prefill(steps, warmup, cpu_baseline):
         "ms_per_step": wall_ms,
         "config": {"workload": "cache-latent prefill fwd (benchmark config 2)", "batch": B, "heads": H,
                    "seq_len": S, "d_qk": 576, "d_v": 512, "causal": True, "softmax_scale": SCALE},
-        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": _load_traffic("prefill"),
-                     "kernel": "mqa_fwd_kernel<false>", "kernel_ms": kern_ms,
-                     "algorithmic_flops_per_launch": flops},
+        "roofline": _roofline("mfma", flops, ks, PEAK_BF16_TFLOPS, "TFLOP/s", _load_traffic("prefill"),
+                              "mqa_fwd_kernel<false>", "algorithmic_flops_per_launch"),
     }
     if cpu_baseline:
         res["cpu_baseline"] = cpu_prefill(q.cpu(), k.cpu(), cpu_baseline)
@@ -118,6 +128,28 @@ def _cpu_threads():
     except AttributeError:
         n = os.cpu_count() or 1
     return max(1, min(n, 16))
+
+
+def _host_info():
+    """The GPU box's host as the CPU baseline saw it: logical CPUs, the affinity set this process
+    may use, the threads torch used and the CPU model name."""
+    import torch
+
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = None
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_count": os.cpu_count(), "affinity": affinity, "torch_threads": torch.get_num_threads(),
+            "cpu_model": model}
 
 
 def _time_repeated(fn, budget_s):
@@ -143,7 +175,7 @@ def cpu_prefill(q, k, budget_s):
     flops = B * H * S * (S + 1) * (576 + 512)
     R.dmla_fwd_cache_latent(qs[:1, :, :256], ks[:1, :256], 512, SCALE, True)  # warm-up
     n, t = _time_repeated(lambda: R.dmla_fwd_cache_latent(qs, ks, 512, SCALE, True), budget_s)
-    return {"value": n * flops / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+    return {"value": n * flops / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port", "host": _host_info(),
             "sample": f"all of config 2 ({B}x{H} heads x {S} causal) through the fp32 eager oracle, "
                       f"{n} passes in {t:.1f} s",
             "seconds": t}
@@ -183,8 +215,7 @@ def bench_decode(steps, warmup, cpu_baseline):
         r = i % 3
         ops.flash_dmla_decode_paged(q, pools[r], tables[r], sl, 512, SCALE)
 
-    wall_ms, kern_ms = _time_launches(step, steps, warmup)
-    achieved = bytes_total / (kern_ms * 1e-3) / 1e9
+    wall_ms, ks = _time_launches(step, steps, warmup)
     res = {
         "metric": "DMLA paged decode KV GB/s (config 3)",
         "value": bytes_total / (wall_ms * 1e-3) / 1e9,
@@ -192,10 +223,8 @@ def bench_decode(steps, warmup, cpu_baseline):
         "ms_per_step": wall_ms,
         "config": {"workload": "paged decode (benchmark config 3)", "batch": B, "heads": H, "page": P,
                    "ctx_sum": int(lens.sum()), "ctx_min": int(lens.min()), "ctx_max": int(lens.max())},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": _load_traffic("decode"),
-                     "kernel": "mqa_fwd_kernel<true> + lse_combine_kernel", "kernel_ms": kern_ms,
-                     "algorithmic_bytes_per_launch": bytes_total},
+        "roofline": _roofline("hbm", bytes_total, ks, PEAK_HBM_GBS, "GB/s", _load_traffic("decode"),
+                              "mqa_fwd_kernel<true> + lse_combine_kernel", "algorithmic_bytes_per_launch"),
     }
     if cpu_baseline:
         res["cpu_baseline"] = cpu_decode(q.cpu(), pools[0].cpu(), tables[0].cpu(), lens.to(torch.int32), bytes_total,
@@ -214,7 +243,7 @@ def cpu_decode(q, pool, table, lens, bytes_total, budget_s):
     qf = q.float()
     R.dmla_decode_paged(qf[:1], pool, table[:1], lens[:1], 512, SCALE)  # warm-up
     n, t = _time_repeated(lambda: R.dmla_decode_paged(qf, pool, table, lens, 512, SCALE), budget_s)
-    return {"value": n * bytes_total / t / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+    return {"value": n * bytes_total / t / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port", "host": _host_info(),
             "sample": f"all of config 3 ({q.shape[0]} sequences, ctx sum {int(lens.sum())}) through the fp32 "
                       f"eager oracle, {n} passes in {t:.1f} s",
             "seconds": t}
@@ -241,8 +270,7 @@ def bench_onthefly(steps, warmup, cpu_baseline):
     def step(i=0):
         ops.flash_dmla_fwd_onthefly(q, k, v, wk, wv, 0.125, True)
 
-    wall_ms, kern_ms = _time_launches(step, steps, warmup)
-    achieved = flops / (kern_ms * 1e-3) / 1e12
+    wall_ms, ks = _time_launches(step, steps, warmup)
     res = {
         "metric": "DMLA on-the-fly prefill TFLOP/s (config 4)",
         "value": flops / (wall_ms * 1e-3) / 1e12,
@@ -250,9 +278,8 @@ def bench_onthefly(steps, warmup, cpu_baseline):
         "ms_per_step": wall_ms,
         "config": {"workload": "on-the-fly prefill fwd (benchmark config 4)", "batch": B, "heads": H, "seq_len": S,
                    "d_in": 128, "d_lat": 64, "causal": True, "softmax_scale": 0.125},
-        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": _load_traffic("onthefly"),
-                     "kernel": "otf_fwd_kernel", "kernel_ms": kern_ms, "algorithmic_flops_per_launch": flops},
+        "roofline": _roofline("mfma", flops, ks, PEAK_BF16_TFLOPS, "TFLOP/s", _load_traffic("onthefly"),
+                              "otf_fwd_kernel", "algorithmic_flops_per_launch"),
     }
     if cpu_baseline:
         res["cpu_baseline"] = cpu_onthefly(q.cpu(), k.cpu(), v.cpu(), wk.cpu(), wv.cpu(), flops, cpu_baseline)
@@ -269,7 +296,7 @@ def cpu_onthefly(q, k, v, wk, wv, flops, budget_s):
     qf, kf, vf, wkf, wvf = q[:1].float(), k[:1].float(), v[:1].float(), wk.float(), wv.float()
     n, t = _time_repeated(lambda: R.dmla_fwd_onthefly(qf, kf, vf, wkf, wvf, 0.125, True), budget_s)
     return {"value": n * flops / q.shape[0] / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port", "sample": f"config 4 batch element 0 through the fp32 eager oracle, {n} passes in {t:.1f} s",
+            "kind": "port", "host": _host_info(), "sample": f"config 4 batch element 0 through the fp32 eager oracle, {n} passes in {t:.1f} s",
             "seconds": t}
 
 
@@ -290,8 +317,7 @@ def bench_bwd(steps, warmup, cpu_baseline):
     def step(i=0):
         ops.flash_dmla_bwd(q, k, o, do, m, l, 512, SCALE, True)
 
-    wall_ms, kern_ms = _time_launches(step, steps, warmup)
-    achieved = flops / (kern_ms * 1e-3) / 1e12
+    wall_ms, ks = _time_launches(step, steps, warmup)
     res = {
         "metric": "DMLA backward TFLOP/s (cache-latent, config 5)",
         "value": flops / (wall_ms * 1e-3) / 1e12,
@@ -299,10 +325,8 @@ def bench_bwd(steps, warmup, cpu_baseline):
         "ms_per_step": wall_ms,
         "config": {"workload": "cache-latent backward (benchmark config 5)", "batch": B, "heads": H, "seq_len": S,
                    "d_qk": 576, "d_v": 512, "causal": True, "softmax_scale": SCALE},
-        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": _load_traffic("bwd"),
-                     "kernel": "bwd_prep + bwd_kt + bwd_dkdv + bwd_dq + bwd_dk_reduce", "kernel_ms": kern_ms,
-                     "algorithmic_flops_per_launch": flops},
+        "roofline": _roofline("mfma", flops, ks, PEAK_BF16_TFLOPS, "TFLOP/s", _load_traffic("bwd"),
+                              "bwd_prep + bwd_kt + bwd_dkdv + bwd_dq + bwd_dk_reduce", "algorithmic_flops_per_launch"),
     }
     if cpu_baseline:
         res["cpu_baseline"] = cpu_bwd(q.cpu(), k.cpu(), o.cpu(), do.cpu(), m.cpu(), l.cpu(), flops, cpu_baseline)
@@ -318,7 +342,7 @@ def cpu_bwd(q, k, o, do, m, l, flops, budget_s):
     torch.set_num_threads(_cpu_threads())
     qf, kf, of, dof = q.float(), k.float(), o.float(), do.float()
     n, t = _time_repeated(lambda: R.dmla_bwd_cache_latent(qf, kf, of, dof, m, l, 512, SCALE, True), budget_s)
-    return {"value": n * flops / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+    return {"value": n * flops / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port", "host": _host_info(),
             "sample": f"all of config 5 through the fp32 eager oracle backward, {n} passes in {t:.1f} s",
             "seconds": t}
 
@@ -348,8 +372,7 @@ def bench_onthefly_bwd(steps, warmup, cpu_baseline):
     def step(i=0):
         ops.flash_dmla_bwd_onthefly(q, k, v, wk, wv, o, do, m, l, 0.125, True)
 
-    wall_ms, kern_ms = _time_launches(step, steps, warmup)
-    achieved = flops / (kern_ms * 1e-3) / 1e12
+    wall_ms, ks = _time_launches(step, steps, warmup)
     res = {
         "metric": "DMLA on-the-fly backward TFLOP/s (config-4 shapes)",
         "value": flops / (wall_ms * 1e-3) / 1e12,
@@ -357,10 +380,8 @@ def bench_onthefly_bwd(steps, warmup, cpu_baseline):
         "ms_per_step": wall_ms,
         "config": {"workload": "on-the-fly backward at the benchmark config 4 shapes", "batch": B, "heads": H,
                    "seq_len": S, "d_in": 128, "d_lat": 64, "causal": True, "softmax_scale": 0.125},
-        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": _load_traffic("onthefly_bwd"),
-                     "kernel": "otf_bwd_prep + proj + dkdv + dq + wgrad + wreduce", "kernel_ms": kern_ms,
-                     "algorithmic_flops_per_launch": flops},
+        "roofline": _roofline("mfma", flops, ks, PEAK_BF16_TFLOPS, "TFLOP/s", _load_traffic("onthefly_bwd"),
+                              "otf_bwd_prep + proj + dkdv + dq + wgrad + wreduce", "algorithmic_flops_per_launch"),
     }
     if cpu_baseline:
         res["cpu_baseline"] = cpu_onthefly_bwd([t.cpu() for t in (q, k, v, wk, wv, o, do, m, l)], flops,
@@ -380,7 +401,7 @@ def cpu_onthefly_bwd(ts, flops, budget_s):
     xs = [q[:1].float(), k[:1].float(), v[:1].float(), wk.float(), wv.float(), o[:1].float(), do[:1].float(),
           m[:1], l[:1]]
     n, t = _time_repeated(lambda: R.dmla_bwd_onthefly(*xs, 0.125, True), budget_s)
-    return {"value": n * flops / B / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+    return {"value": n * flops / B / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port", "host": _host_info(),
             "sample": f"batch element 0 of the config-4 shapes through the fp32 eager oracle backward, "
                       f"{n} passes in {t:.1f} s",
             "seconds": t}

@@ -202,6 +202,9 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   int seg_pages[2] = {0, 0};
   if constexpr (kDecode) {
     const int npg = (tile_end + (kPage / kTileN) - 1) / (kPage / kTileN) - wk.page_begin;
+    // The plan keeps segments within the two page registers (decode_ranges); a segment past
+    // them would read wrapped (valid but wrong) pages, so its output is poisoned instead.
+    bad_page = npg > kMaxSegPages;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
       if (64 * h + lane < npg) seg_pages[h] = p.block_table[b * p.bt_sb + wk.page_begin + 64 * h + lane];
@@ -1010,12 +1013,16 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const int32_t
 }
 
 // Ranges of a decode plan: one workgroup per range and head group fills the CUs; more ranges
-// when the widest batch would overflow a segment's page cache.
+// when the widest batch would overflow a segment's page cache.  A segment spans at most W
+// tiles, W = ceil(weighted / R), and the weighted total is at most B max_pages 2 + kSegCost B
+// (every sequence full and nonempty), so R >= that bound / kMaxSegTiles keeps W <= kMaxSegTiles
+// and every segment within kMaxSegPages pages (a segment may start on the second tile of a page).
 int64_t decode_ranges(int64_t B, int64_t H, int64_t max_pages) {
   const int64_t hg = (H + kRowsPerWG - 1) / kRowsPerWG;
   int64_t r = device_cu_count() / hg;
   if (r >= 8) r -= r % 8;
-  const int64_t cap = (B * max_pages * (kPage / kTileN) + kMaxSegTiles - 1) / kMaxSegTiles;
+  const int64_t weighted_max = B * max_pages * (kPage / kTileN) + (int64_t)kSegCost * B;
+  const int64_t cap = (weighted_max + kMaxSegTiles - 1) / kMaxSegTiles;
   return std::max<int64_t>(std::max<int64_t>(r, cap), 1);
 }
 

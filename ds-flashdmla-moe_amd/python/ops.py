@@ -49,6 +49,15 @@ def _check_bf16(name: str, t: torch.Tensor, ndim: int) -> None:
     _require(t.stride(-1) == 1, f"{name} must be contiguous in its last dim")
 
 
+def _check_fp16_range(name: str, t: torch.Tensor) -> None:
+    """Raises unless every entry of t is finite and inside fp16's range (|x| <= 65504): the
+    kernels convert these operands to fp16, which saturates beyond it.  One device sync."""
+    if t.numel() == 0:
+        return
+    _require(bool(torch.isfinite(t).all()) and float(t.abs().max()) <= 65504.0,
+             f"{name} has entries outside fp16's finite range (|x| <= 65504)")
+
+
 def _scale(softmax_scale: Optional[float], d_qk: int) -> float:
     return float(softmax_scale) if softmax_scale is not None else 1.0 / math.sqrt(d_qk)
 
@@ -98,11 +107,16 @@ def flash_dmla_fwd_onthefly(
     softmax_scale: Optional[float] = None,
     causal: bool = True,
     return_stats: bool = False,
+    check_range: bool = False,
 ):
     """On-the-fly DMLA forward: K_lat = K WK and V_lat = V WV per head inside the kernel.
 
     q [B, H, Sq, 64]; k, v [B, Sk, H, 128]; wk, wv [H, 128, 64] (all bf16).  Returns o
     [B, H, Sq, 64] bf16, or (o, m, l) with return_stats.  softmax_scale defaults to 1/sqrt(64).
+    The attention products run on fp16 operands: q is converted to fp16 (exact for bf16 values
+    inside fp16's range, saturating beyond 65504), and K_lat (times scale*log2 e), V_lat and P
+    are rounded to fp16.  Inputs must be finite.  check_range=True verifies on the host (one
+    device sync) that q, k, v, wk, wv are finite and within fp16's range.
     """
     _check_bf16("q", q, 4)
     for name, t in (("k", k), ("v", v)):
@@ -116,6 +130,9 @@ def flash_dmla_fwd_onthefly(
     _require(tuple(wk.shape) == (H, Din, Dl) and tuple(wv.shape) == (H, Din, Dl),
              "wk and wv must be [H, d_in, d_lat]")
     _require(wk.stride() == wv.stride(), "wk and wv must share strides")
+    if check_range:
+        for name, t in (("q", q), ("k", k), ("v", v), ("wk", wk), ("wv", wv)):
+            _check_fp16_range(name, t)
     o = torch.empty((B, H, Sq, Dl), dtype=torch.bfloat16, device=q.device)
     m = l = None
     if return_stats:
@@ -354,8 +371,7 @@ def flash_dmla_bwd(
                  f"{name} must be a contiguous float32 GPU tensor [B, H, Sq]")
     if check_range:
         for name, t in (("q", q), ("k_lat", k_lat), ("do", do)):
-            _require(bool(torch.isfinite(t).all()) and float(t.abs().max()) <= 65504.0,
-                     f"{name} has entries outside fp16's finite range (|x| <= 65504)")
+            _check_fp16_range(name, t)
     dq_dtype = q.dtype if dq_dtype is None else dq_dtype
     _require(dq_dtype in (torch.bfloat16, torch.float32) and dk_dtype in (torch.bfloat16, torch.float32),
              "gradient dtypes must be bfloat16 or float32")
@@ -420,8 +436,7 @@ def flash_dmla_bwd_onthefly(
                  f"{name} must be a contiguous float32 GPU tensor [B, H, Sq]")
     if check_range:
         for name, t in (("q", q), ("k", k), ("v", v), ("do", do), ("wk", wk), ("wv", wv)):
-            _require(bool(torch.isfinite(t).all()) and float(t.abs().max()) <= 65504.0,
-                     f"{name} has entries outside fp16's finite range (|x| <= 65504)")
+            _check_fp16_range(name, t)
     dq = torch.empty((B, H, Sq, Dl), dtype=torch.bfloat16, device=q.device)
     dk = torch.empty((B, Sk, H, Din), dtype=torch.bfloat16, device=q.device)
     dv = torch.empty_like(dk)

@@ -237,6 +237,38 @@ def decode_plan(cache_seqlens, n_ranges: int, max_pages: int, page_size: int = 6
     return [B, R, W, total, sb[-1], seg_cost, 0, 0] + tp + sb + ns + fr + rs + rfb
 
 
+def decode_ranges(B: int, H: int, max_pages: int, cu_count: int, page_size: int = 64, tile: int = 32,
+                  seg_cost: int = 16, max_seg_pages: int = 128) -> int:
+    """Range count R of a decode plan (no reference counterpart): one range per CU and group of
+    64 heads (a multiple of 8 from 8 on), raised so that a range spans at most
+    2*max_seg_pages - 2 tiles when every sequence is full."""
+    hg = -(-H // 64)
+    r = cu_count // hg
+    if r >= 8:
+        r -= r % 8
+    max_seg_tiles = 2 * max_seg_pages - 2
+    weighted_max = B * max_pages * (page_size // tile) + seg_cost * B
+    return max(r, -(-weighted_max // max_seg_tiles), 1)
+
+
+def plan_segment_pages(plan, cache_seqlens, page_size: int = 64, tile: int = 32):
+    """Pages spanned by each (range, sequence) segment of a decode plan, as the decode kernel
+    walks them: the segment's tiles [s0, s1) of sequence b cover pages s0//2 .. ceil(s1/2)-1."""
+    B = len(cache_seqlens)
+    R = plan[1]
+    tp = plan[8:8 + B + 1]
+    rs = plan[8 + 4 * B + 2:8 + 4 * B + 2 + R + 1]
+    per = page_size // tile
+    out = []
+    for r in range(R):
+        t0, t1 = rs[r], rs[r + 1]
+        for b in range(B):
+            s0, s1 = max(t0, tp[b]) - tp[b], min(t1, tp[b + 1]) - tp[b]
+            if s0 < s1:
+                out.append(-(-s1 // per) - s0 // per)
+    return out
+
+
 def kv_append(kv_pool: Tensor, block_table: Tensor, cache_seqlens: Tensor, new_kv: Tensor,
               new_lens: Optional[Tensor] = None) -> Tensor:
     """Paged KV-cache append (no reference counterpart; the producer side of gather_pages).

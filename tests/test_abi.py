@@ -217,3 +217,19 @@ def test_onthefly_bwd_python_wrapper_rejects_cpu_tensors():
     m = torch.zeros(1, 2, 4)
     with pytest.raises(ValueError, match="GPU tensor"):
         ops.flash_dmla_bwd_onthefly(q, k, k, w, w, q, q, m, m)
+
+
+def test_fp16_range_check_rejects_values_the_kernels_would_saturate():
+    # The on-the-fly forward and both backwards convert their operands to fp16; with
+    # check_range=True the wrappers refuse inputs beyond fp16's range or non-finite ones.
+    ok = torch.tensor([0.5, -65280.0, 3.0])  # the largest bf16 below 65504.to(torch.bfloat16)
+    ops._check_fp16_range("q", ok)
+    ops._check_fp16_range("q", ok[:0])
+    for bad in ([1.0, 70000.0], [float("nan"), 1.0], [-float("inf")]):
+        with pytest.raises(ValueError, match="fp16's finite range"):
+            ops._check_fp16_range("q", torch.tensor(bad).to(torch.bfloat16))
+
+
+def test_onthefly_forward_wrapper_takes_check_range():
+    import inspect
+    assert "check_range" in inspect.signature(ops.flash_dmla_fwd_onthefly).parameters

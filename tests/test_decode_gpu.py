@@ -99,6 +99,18 @@ def test_decode_config3_full_shape(gpu):
     _check(gpu, q, pool, table, sl, oracle_device="gpu")
 
 
+@pytest.mark.gpu
+def test_decode_long_contexts_stay_within_segment_pages(gpu):
+    # 64 full 16K-token sequences: the plan's ranges must keep each segment within the 128 page
+    # indices a workgroup holds (a range count sized from the tiles alone made 130-page segments
+    # that read wrapped page indices).  The plan stored by the kernel is checked page by page.
+    lens = [16384] * 64
+    q, pool, table, sl = _paged(lens, 128, seed=21, poison_tail=False)
+    _check(gpu, q, pool, table, sl, oracle_device="gpu")
+    plan = ops.flash_dmla_decode_plan(sl.to(gpu), 128, table.shape[1]).cpu().tolist()
+    assert max(R.plan_segment_pages(plan, lens)) <= 128
+
+
 def _lse_close(lse, lse_ref, tol=1e-3):
     lse, lse_ref = lse.cpu(), lse_ref.cpu()
     inf = torch.isinf(lse_ref)

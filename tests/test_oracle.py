@@ -396,6 +396,34 @@ def test_decode_plan_balances_tiles_plus_segment_costs():
     assert max(cost) <= W + 16 and min(c for c in cost if c) >= W - 16 - 16
 
 
+@pytest.mark.parametrize("cus", [256, 304, 80])
+@pytest.mark.parametrize("H", [128, 16, 200])
+def test_decode_segments_fit_the_page_registers(cus, H):
+    """The decode kernel holds a segment's page indices in two VGPRs (128 pages): with the range
+    count of decode_ranges no segment of any plan spans more, over full and ragged batches."""
+    g = torch.Generator().manual_seed(cus + H)
+    for B in (1, 7, 64, 128, 300):
+        for max_pages in (1, 2, 127, 128, 129, 256, 1000):
+            R_ = R.decode_ranges(B, H, max_pages, cus)
+            full = [max_pages * 64] * B
+            ragged = torch.randint(0, max_pages * 64 + 1, (B,), generator=g).tolist()
+            for lens in (full, ragged):
+                plan = R.decode_plan(lens, R_, max_pages)
+                pages = R.plan_segment_pages(plan, lens)
+                assert max(pages, default=0) <= 128, (B, H, max_pages, R_, max(pages))
+
+
+def test_decode_range_bound_without_segment_costs_overflows():
+    # Planted mistake: sizing R from the tiles alone (no per-segment weight) lets the ranges of
+    # 64 full 16K-token sequences on 256 CUs span 130 pages, which the check above rejects.
+    B, H, max_pages, cus = 64, 128, 256, 256
+    r = (cus // 2) - (cus // 2) % 8
+    bad_R = max(r, -(-(B * max_pages * 2) // 254))
+    plan = R.decode_plan([max_pages * 64] * B, bad_R, max_pages)
+    assert max(R.plan_segment_pages(plan, [max_pages * 64] * B)) > 128
+    assert R.decode_ranges(B, H, max_pages, cus) > bad_R
+
+
 def test_attention_with_no_keys_is_the_fully_masked_case():
     q = torch.randn(2, 3, 8, dtype=torch.float64)
     k = torch.zeros(2, 0, 8, dtype=torch.float64)
