@@ -12,11 +12,14 @@
 //     once per key tile for all 512 rows, so the projection adds 1/4 to the attention MFMAs
 //     (a 128-row tile would double them);
 //   * tile t is attended: S^T = K_lat Q^T (Q in registers), P in the exp2 domain, O += P V_lat.
-// K_lat, V_lat, Q and P enter the attention products as fp16 (Q converted exactly, the rest
-// rounded from fp32): 3 more significand bits than bf16, which keeps the rounding of the
-// latent tiles well inside the output tolerance even for rows that see only a few keys.
-// K_lat is stored multiplied by scale log2(e) and the score accumulators start at -m_ref, so
-// the MFMA hands the softmax its exp2 arguments directly.
+// Scores: Q stays in bf16 (exact) and K_lat, multiplied by scale log2(e), is stored as a bf16
+// pair hi + lo (hi = bf16(c), lo = bf16(c - hi)), two bf16 MFMAs per k-step: the scores carry
+// ~2^-17 relative error, where one fp16 rounding of K_lat (2^-12) moved the row statistics
+// m, l by ~1.7e-3 at the benchmark's config 4.  (An fp16 pair does not work: most residuals
+// are fp16 subnormals, which the fp16 MFMA loses.)  V_lat and P enter the PV product as fp16,
+// rounded from fp32: 3 more significand bits than bf16, which keeps their rounding well inside
+// the output tolerance even for rows that see only a few keys.  The score accumulators start
+// at -m_ref, so the MFMA hands the softmax its exp2 arguments directly.
 // Every MFMA operand read from LDS is a conflict-free 16-byte read: K_lat rows for S^T and a
 // V_lat^T tile whose key order matches the C layout of S^T (so P needs no transposition).
 //
@@ -38,14 +41,16 @@ constexpr int kOtfThreads = 64 * kOtfWaves;
 constexpr int kOtfRows = 64 * kOtfWaves;   // 512 query rows per workgroup
 constexpr int kOtfKeys = 64;               // keys per tile
 constexpr float kSlack = 8.0f;             // log2 slack of the reference max
-// LDS: W^T (2 x 64 x 128 bf16), raw K / V stages (2 x 2 x 64 x 128), K_lat and V_lat^T (2 x 2 x 64 x 64)
+// LDS: W^T (2 x 64 x 128 bf16), raw K / V stages (2 x 2 x 64 x 128), K_lat hi and V_lat^T
+// (2 x 2 x 64 x 64), K_lat lo (2 x 64 x 64)
 constexpr int kWBytes = kDlat * kDin * 2;          // 16 KB
 constexpr int kRawBytes = kOtfKeys * kDin * 2;     // 16 KB
 constexpr int kLatBytes = kOtfKeys * kDlat * 2;    // 8 KB
 constexpr int kWOff = 0;                           // [WK^T, WV^T]
 constexpr int kRawOff = 2 * kWBytes;               // [stage][K, V]
 constexpr int kLatOff = kRawOff + 4 * kRawBytes;   // [buffer][K_lat, V_lat^T]
-constexpr int kOtfLds = kLatOff + 4 * kLatBytes;   // 128 KB
+constexpr int kLatLoOff = kLatOff + 4 * kLatBytes; // [buffer] K_lat lo
+constexpr int kOtfLds = kLatLoOff + 2 * kLatBytes; // 144 KB
 static_assert(kOtfLds <= 160 * 1024, "LDS budget");
 
 struct OtfParams {
@@ -127,15 +132,14 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
   if (n_t > 1) stage_raw(1, 1);
 
   // ---- Q rows of this wave as the B operand of S^T: qreg[rb][ks] = Q[row0 + 16 rb + l16][32 ks + 8 g ..]
-  f16x8 qreg[4][2];
+  bf16x8 qreg[4][2];
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb) {
     const int r = min(row0 + 16 * rb + l16, p.Sq - 1);
     const bf16* qrow = p.q + b * p.q_sb + h * p.q_sh + (int64_t)r * p.q_ss + 8 * g;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + 32 * ks);
-      qreg[rb][ks] = bf16_to_f16(__builtin_shufflevector(x, x, 0, 1, 2, 3), __builtin_shufflevector(x, x, 4, 5, 6, 7));
+      qreg[rb][ks] = *reinterpret_cast<const bf16x8*>(qrow + 32 * ks);
     }
   }
   wait_vmem();
@@ -167,16 +171,24 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
           if constexpr (kK) c = mfma_bf16(wreg[ks], x, c);   // K_lat^T[dim 16 pdb + 4g + i][key 16 kb + l16]
           else c = mfma_bf16(x, wreg[ks], c);                // V_lat[key 16 kb + 4g + i][dim 16 pdb + l16]
         }
-        // K_lat is stored pre-multiplied by scale log2(e), so that scores come out of the MFMA in
-        // log2 units (one fp16 rounding either way).
-        if constexpr (kK) c *= p.scale_log2;
-        f16x4 v;
-        v[0] = (_Float16)c[0]; v[1] = (_Float16)c[1]; v[2] = (_Float16)c[2]; v[3] = (_Float16)c[3];
         if constexpr (kK) {
+          // K_lat is stored pre-multiplied by scale log2(e), so that scores come out of the MFMA
+          // in log2 units, as hi + lo with hi = bf16(c) and lo = bf16(c - hi):
           // K_lat[key 16 kb + l16][dims 16 pdb + 4g .. +3]
+          c *= p.scale_log2;
+          bf16x4 hi, lo;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            hi[i] = (bf16)c[i];
+            lo[i] = (bf16)(c[i] - (float)hi[i]);
+          }
           const int key = 16 * kb + l16;
-          *reinterpret_cast<DMLA_LDS f16x4*>(lat + lat_off(key, 2 * pdb + (g >> 1)) + 8 * (g & 1)) = v;
+          const int o = lat_off(key, 2 * pdb + (g >> 1)) + 8 * (g & 1);
+          *reinterpret_cast<DMLA_LDS bf16x4*>(lat + o) = hi;
+          *reinterpret_cast<DMLA_LDS bf16x4*>(lds + kLatLoOff + lb * kLatBytes + o) = lo;
         } else {
+          f16x4 v;
+          v[0] = (_Float16)c[0]; v[1] = (_Float16)c[1]; v[2] = (_Float16)c[2]; v[3] = (_Float16)c[3];
           // V_lat^T[dim 16 pdb + l16][position]: keys 4g + i of key block kb sit at positions
           // 32 (kb/2) + 8 g + 4 (kb&1) + i, the key order of the P operand (S^T C layout).
           const int dim = 16 * pdb + l16;
@@ -213,6 +225,7 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
 
     const DMLA_LDS char* klat = lds + kLatOff + ((t & 1) * 2) * kLatBytes;
     const DMLA_LDS char* vlat = klat + kLatBytes;
+    const DMLA_LDS char* klo = lds + kLatLoOff + (t & 1) * kLatBytes;
     // x[kb][rb] = S^T in log2 units minus the row's reference: keys 16 kb + 4g + i, row 16 rb +
     // l16.  The MFMA accumulators start at -m_ref (0 while a row has no reference), so x is the
     // exp2 argument as it leaves the matrix core.
@@ -222,12 +235,17 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
     f32x4 s[4][4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      const f16x8 k0 = *reinterpret_cast<const DMLA_LDS f16x8*>(klat + lat_off(16 * kb + l16, g));
-      const f16x8 k1 = *reinterpret_cast<const DMLA_LDS f16x8*>(klat + lat_off(16 * kb + l16, 4 + g));
+      const int o0 = lat_off(16 * kb + l16, g), o1 = lat_off(16 * kb + l16, 4 + g);
+      const bf16x8 k0 = *reinterpret_cast<const DMLA_LDS bf16x8*>(klat + o0);
+      const bf16x8 k1 = *reinterpret_cast<const DMLA_LDS bf16x8*>(klat + o1);
+      const bf16x8 k0l = *reinterpret_cast<const DMLA_LDS bf16x8*>(klo + o0);
+      const bf16x8 k1l = *reinterpret_cast<const DMLA_LDS bf16x8*>(klo + o1);
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb) {
-        s[kb][rb] = mfma_f16(k0, qreg[rb][0], f32x4{nmr[rb], nmr[rb], nmr[rb], nmr[rb]});
-        s[kb][rb] = mfma_f16(k1, qreg[rb][1], s[kb][rb]);
+        s[kb][rb] = mfma_bf16(k0l, qreg[rb][0], f32x4{nmr[rb], nmr[rb], nmr[rb], nmr[rb]});
+        s[kb][rb] = mfma_bf16(k1l, qreg[rb][1], s[kb][rb]);
+        s[kb][rb] = mfma_bf16(k0, qreg[rb][0], s[kb][rb]);
+        s[kb][rb] = mfma_bf16(k1, qreg[rb][1], s[kb][rb]);
       }
     }
     // Only tiles that reach past some row's limit or past Sk are masked, in a block of their own.

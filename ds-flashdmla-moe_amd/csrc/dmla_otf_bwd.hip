@@ -12,7 +12,7 @@
 // Seven kernels run in order on one stream, all deterministic (no atomics):
 //   otf_bwd_prep_kernel    per query row: Q and dO as fp16, lse2 = (m + ln l) log2(e), D;
 //   otf_bwd_wt_kernel      WK^T and WV^T;
-//   otf_bwd_proj_kernel    K_lat and V_lat as fp16 (the forward's projection, same values);
+//   otf_bwd_proj_kernel    K_lat and V_lat as fp16 (the forward's projection products);
 //   otf_bwd_dkdv_kernel    per 128 keys: dK_lat, dV_lat over the rows that see them;
 //   otf_bwd_dq_kernel      per 128 rows: dQ over the keys they see (S and dP recomputed);
 //   otf_bwd_wgrad_kernel   per (tensor, head, 1024 keys): dK / dV and a dWK / dWV partial;
@@ -20,8 +20,11 @@
 //
 // Every product runs on v_mfma_f32_16x16x32_f16 with fp32 accumulation: Q, dO, K, V and the
 // weights are converted to fp16 exactly (bf16's significand fits fp16's; |x| <= 65504), and the
-// rounded intermediates (K_lat, V_lat, P, dS, dK_lat, dV_lat) are fp16 -- as in the forward,
-// whose K_lat / V_lat this backward recomputes with the same operands in the same order.  The one layout trick used
+// rounded intermediates (K_lat, V_lat, P, dS, dK_lat, dV_lat) are fp16.  V_lat equals the
+// forward's (same operands, same order, same rounding); K_lat is the forward's fp32 projection
+// rounded once to fp16, where the forward keeps a bf16 hi + lo pair for its scores, so the
+// recomputed P carries the fp16 rounding of the scores (~2^-12 relative) against the forward's
+// exact statistics -- well inside the gradients' tolerance.  The one layout trick used
 // throughout: an MFMA C tile (lane l holds rows 4(l/16)+i, column l%16) of two 16-row blocks is
 // the B operand of a product contracting over those 32 rows when the k-index runs over rows
 // {4g+i} then {16+4g+i} (g = l/16); ds_read_b64_tr_b16 on a row-major tile hands the A operand

@@ -113,10 +113,10 @@ def flash_dmla_fwd_onthefly(
 
     q [B, H, Sq, 64]; k, v [B, Sk, H, 128]; wk, wv [H, 128, 64] (all bf16).  Returns o
     [B, H, Sq, 64] bf16, or (o, m, l) with return_stats.  softmax_scale defaults to 1/sqrt(64).
-    The attention products run on fp16 operands: q is converted to fp16 (exact for bf16 values
-    inside fp16's range, saturating beyond 65504), and K_lat (times scale*log2 e), V_lat and P
-    are rounded to fp16.  Inputs must be finite.  check_range=True verifies on the host (one
-    device sync) that q, k, v, wk, wv are finite and within fp16's range.
+    The scores take q as given (bf16) against K_lat * scale * log2(e) kept as a bf16 hi + lo
+    pair; V_lat and P enter the PV product as fp16 (V_lat saturates beyond 65504).  Inputs must
+    be finite.  check_range=True verifies on the host (one device sync) that q, k, v, wk, wv
+    are finite and within fp16's range (the backward converts all of them to fp16).
     """
     _check_bf16("q", q, 4)
     for name, t in (("k", k), ("v", v)):

@@ -78,10 +78,15 @@ int dmla_fwd_cache_latent(const void* q, const void* k_lat, void* o, float* m, f
  *   o      [B, H, Sq, d_lat]   bf16  strides (o_sb, o_sh, o_ss)
  *   m, l   [B, H, Sq]          fp32  contiguous; may both be NULL
  *
- *   K_lat[b,h] = k[b,:,h,:] wk[h] and V_lat[b,h] = v[b,:,h,:] wv[h] (rounded to fp16 inside
- *   the kernel), then o = softmax(softmax_scale q K_lat^T (+ causal mask)) V_lat with the
- *   statistics of dmla_fwd_cache_latent (natural-log units; m = -inf, l = 0, o = 0 for a row
- *   without an unmasked key).  causal != 0 masks key j > i + (Sk - Sq).
+ *   K_lat[b,h] = k[b,:,h,:] wk[h] and V_lat[b,h] = v[b,:,h,:] wv[h] inside the kernel, then
+ *   o = softmax(softmax_scale q K_lat^T (+ causal mask)) V_lat with the statistics of
+ *   dmla_fwd_cache_latent (natural-log units; m = -inf, l = 0, o = 0 for a row without an
+ *   unmasked key).  causal != 0 masks key j > i + (Sk - Sq).
+ *   Precision: the scores take q as given (bf16) against K_lat * softmax_scale * log2(e) kept
+ *   as a bf16 pair hi + lo (~2^-17 relative); V_lat and the probabilities P enter the PV
+ *   product as fp16 (V_lat saturates beyond |65504|).  Inputs must be finite: the kernel is
+ *   built without NaN handling in its max reductions, so a NaN input gives unspecified (not
+ *   necessarily NaN) outputs in the rows it reaches.
  * Supported: d_in = 128, d_lat = 64.
  */
 int dmla_fwd_onthefly(const void* q, const void* k, const void* v, const void* wk, const void* wv,

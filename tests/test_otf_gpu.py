@@ -1,9 +1,11 @@
 """Parity of the on-the-fly forward (dmla_fwd_onthefly) with the fp32 oracle.
 
 The oracle projects K_lat = K WK and V_lat = V WV in fp32 and runs exact attention; the kernel
-projects on MFMA and rounds K_lat / V_lat (and P) to fp16 before the attention products, which
-the north-star tolerance (max-abs 2e-2, mean-rel 1e-2) covers.  Inputs follow benchmark config 4:
-q, k, v ~ N(0, 1), wk and wv Xavier-uniform (bound sqrt(6 / (128 + 64))), scale 1/8.
+projects on MFMA, rounds V_lat and P to fp16 before the PV product and keeps K_lat as an fp16
+hi + lo pair for the scores.  Outputs are held to the north-star tolerance (max-abs 2e-2,
+mean-rel 1e-2) and the statistics to 1e-3 (m max-abs, l max-rel), as in every other mode.
+Inputs follow benchmark config 4: q, k, v ~ N(0, 1), wk and wv Xavier-uniform (bound
+sqrt(6 / (128 + 64))), scale 1/8.
 """
 import math
 
@@ -34,13 +36,8 @@ def _check(gpu, B, H, Sq, Sk, causal, seed, ref_device="cpu", scale=0.125):
     dev = gpu if ref_device == "gpu" else torch.device("cpu")
     o_ref, m_ref, l_ref = R.dmla_fwd_onthefly(q.to(dev), k.to(dev), v.to(dev), wk.to(dev), wv.to(dev), scale, causal)
     assert_out_close(o, o_ref)
-    # m, l: K_lat is rounded to fp16 inside the kernel, so the scores carry ~2^-12 relative error;
-    # the statistics are checked at 1e-2 (m absolute, l relative).
-    mf = torch.isfinite(m_ref.to(o.device))
-    assert torch.equal(torch.isfinite(m), mf)
-    assert (m[mf] - m_ref.to(o.device)[mf]).abs().max().item() <= 1e-2
-    pos = l_ref.to(o.device) > 0
-    assert ((l[pos] - l_ref.to(o.device)[pos]).abs() / l_ref.to(o.device)[pos]).max().item() <= 1e-2
+    dm, dl = assert_stats_close(m, l, m_ref, l_ref)
+    print(f"on-the-fly B={B} H={H} Sq={Sq} Sk={Sk}: m max-abs {dm:.2e}, l max-rel {dl:.2e}")
     return o
 
 
