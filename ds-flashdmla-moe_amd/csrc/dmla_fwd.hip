@@ -27,6 +27,7 @@
 //  * Softmax in the exp2 domain against a per-row reference max fixed at the first tile: p
 //    stays below 2^kHeadroom, so O is never rescaled.  Scores climbing past that headroom
 //    trigger a recomputation of the row tile from a higher reference.
+#include <mutex>
 #include <type_traits>
 
 #include "dmla_common.h"
@@ -1233,6 +1234,62 @@ extern "C" int dmla_decode_paged_planned(const void* q, const void* kv_pool, con
                        workspace_bytes, (hipStream_t)stream);
 }
 
+namespace dmla {
+namespace {
+
+// The body of dmla_decode_paged on a workspace the caller vouches for (16-byte aligned, at
+// least dmla_decode_workspace_bytes): the plan at its head, the split partials after it.
+int decode_paged_on(const void* q, const void* kv_pool, const int32_t* block_table, const int32_t* cache_seqlens,
+                    void* o, float* lse, int64_t B, int64_t H, int64_t d_v, int64_t num_pages,
+                    int64_t max_pages_per_seq, int64_t q_sb, int64_t q_sh, int64_t kv_sp, int64_t kv_ss,
+                    int64_t bt_sb, int64_t o_sb, int64_t o_sh, float softmax_scale, void* workspace,
+                    int64_t workspace_bytes, hipStream_t stream) {
+  const int64_t pb = dmla_decode_plan_bytes(B, H, max_pages_per_seq);
+  int32_t* plan = static_cast<int32_t*>(workspace);
+  void* parts = static_cast<char*>(workspace) + pb;
+  // Small batches (the serving case): the decode kernel builds the plan itself and stores it in
+  // the workspace; otherwise the plan kernel runs first.
+  if (B <= kInlinePlanB && decode_ranges(B, H, max_pages_per_seq) <= kInlinePlanR)
+    return decode_launch(q, kv_pool, block_table, cache_seqlens, o, lse, B, H, num_pages, max_pages_per_seq, q_sb,
+                         q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale, nullptr, plan, parts,
+                         workspace_bytes - pb, stream);
+  int rc = dmla_decode_plan(cache_seqlens, B, H, max_pages_per_seq, plan, pb, stream);
+  if (rc != DMLA_OK) return rc;
+  return decode_launch(q, kv_pool, block_table, cache_seqlens, o, lse, B, H, num_pages, max_pages_per_seq, q_sb,
+                       q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale, plan, nullptr, parts,
+                       workspace_bytes - pb, stream);
+}
+
+// Scratch of dmla_decode_paged_noalloc: a file-scope device array, one copy per GPU, held until
+// the process ends.  Host code never uses the array's name as an address (on the host it is a
+// stand-in for the symbol); the device address comes from hipGetSymbolAddress, looked up once
+// per device with that device current.
+static __device__ __align__(256) char scratch[DMLA_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_on_current_device(void** out, const char* what) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(DMLA_ERR_HIP, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(DMLA_ERR_UNSUPPORTED, "%s: device %d out of range", what, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(DMLA_ERR_HIP, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return DMLA_OK;
+}
+
+}  // namespace
+}  // namespace dmla
+
 extern "C" int dmla_decode_paged(const void* q, const void* kv_pool, const int32_t* block_table,
                                  const int32_t* cache_seqlens, void* o, float* lse, int64_t B,
                                  int64_t H, int64_t d_qk, int64_t d_v, int64_t page_size,
@@ -1249,18 +1306,31 @@ extern "C" int dmla_decode_paged(const void* q, const void* kv_pool, const int32
     return fail(DMLA_ERR_WORKSPACE, "dmla_decode_paged: workspace of %lld bytes needed (got %lld)",
                 (long long)need, (long long)workspace_bytes);
   if (!aligned16(workspace)) return fail(DMLA_ERR_INVALID_ARG, "dmla_decode_paged: workspace must be 16-byte aligned");
-  const int64_t pb = dmla_decode_plan_bytes(B, H, max_pages_per_seq);
-  int32_t* plan = static_cast<int32_t*>(workspace);
-  void* parts = static_cast<char*>(workspace) + pb;
-  // Small batches (the serving case): the decode kernel builds the plan itself and stores it in
-  // the workspace; otherwise the plan kernel runs first.
-  if (B <= kInlinePlanB && decode_ranges(B, H, max_pages_per_seq) <= kInlinePlanR)
-    return decode_launch(q, kv_pool, block_table, cache_seqlens, o, lse, B, H, num_pages, max_pages_per_seq, q_sb,
-                         q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale, nullptr, plan, parts,
-                         workspace_bytes - pb, (hipStream_t)stream);
-  int rc = dmla_decode_plan(cache_seqlens, B, H, max_pages_per_seq, plan, pb, stream);
+  return decode_paged_on(q, kv_pool, block_table, cache_seqlens, o, lse, B, H, d_v, num_pages, max_pages_per_seq,
+                         q_sb, q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale, workspace, workspace_bytes,
+                         (hipStream_t)stream);
+}
+
+extern "C" int dmla_decode_paged_noalloc(const void* q, const void* kv_pool, const int32_t* block_table,
+                                         const int32_t* cache_seqlens, void* o, float* lse, int64_t B,
+                                         int64_t H, int64_t d_qk, int64_t d_v, int64_t page_size,
+                                         int64_t num_pages, int64_t max_pages_per_seq, int64_t q_sb,
+                                         int64_t q_sh, int64_t kv_sp, int64_t kv_ss, int64_t bt_sb,
+                                         int64_t o_sb, int64_t o_sh, float softmax_scale, dmla_stream_t stream) {
+  clear_error();
+  int rc0 = decode_validate(q, kv_pool, block_table, cache_seqlens, o, B, H, d_qk, d_v, page_size, num_pages,
+                            max_pages_per_seq, q_sb, q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale);
+  if (rc0 != DMLA_OK || B == 0 || H == 0) return rc0;
+  const int64_t need = dmla_decode_workspace_bytes(B, H, d_v, max_pages_per_seq);
+  if (need > DMLA_NOALLOC_SCRATCH_BYTES)
+    return fail(DMLA_ERR_WORKSPACE,
+                "dmla_decode_paged_noalloc: this batch needs %lld bytes of scratch, more than the %lld of the "
+                "static scratch; use dmla_decode_paged with a workspace",
+                (long long)need, (long long)DMLA_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  int rc = scratch_on_current_device(&ws, "dmla_decode_paged_noalloc");
   if (rc != DMLA_OK) return rc;
-  return decode_launch(q, kv_pool, block_table, cache_seqlens, o, lse, B, H, num_pages, max_pages_per_seq, q_sb,
-                       q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale, plan, nullptr, parts,
-                       workspace_bytes - pb, (hipStream_t)stream);
+  return decode_paged_on(q, kv_pool, block_table, cache_seqlens, o, lse, B, H, d_v, num_pages, max_pages_per_seq,
+                         q_sb, q_sh, kv_sp, kv_ss, bt_sb, o_sb, o_sh, softmax_scale, ws, DMLA_NOALLOC_SCRATCH_BYTES,
+                         (hipStream_t)stream);
 }

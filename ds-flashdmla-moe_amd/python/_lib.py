@@ -67,6 +67,13 @@ SIGNATURES = {
         + [_i64] * 7  # q_sb q_sh kv_sp kv_ss bt_sb o_sb o_sh
         + [_f32, _ptr, _i64, _ptr],  # scale, workspace, workspace_bytes, stream
     ),
+    "dmla_decode_paged_noalloc": (
+        _int,
+        [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr]  # q, kv_pool, block_table, seqlens, o, lse
+        + [_i64] * 7  # B, H, d_qk, d_v, page_size, num_pages, max_pages_per_seq
+        + [_i64] * 7  # q_sb q_sh kv_sp kv_ss bt_sb o_sb o_sh
+        + [_f32, _ptr],  # scale, stream
+    ),
     "dmla_decode_plan_bytes": (_i64, [_i64, _i64, _i64]),
     "dmla_decode_plan": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr]),
     "dmla_decode_paged_planned": (

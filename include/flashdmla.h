@@ -129,6 +129,24 @@ int dmla_decode_paged(const void* q, const void* kv_pool, const int32_t* block_t
                       dmla_stream_t stream);
 
 /*
+ * dmla_decode_paged without a workspace, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  Same arguments and results as dmla_decode_paged; the plan
+ * and split partials live in a static device array of DMLA_NOALLOC_SCRATCH_BYTES per GPU
+ * (held until the process ends), and a batch whose dmla_decode_workspace_bytes exceeds it is
+ * rejected with DMLA_ERR_WORKSPACE.  Nothing is allocated and no memory is cleared (every byte
+ * a call reads it has written first).  All calls on one GPU share that GPU's array, so calls
+ * that overlap on one GPU (on different streams, or from several threads) race.
+ */
+#define DMLA_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int dmla_decode_paged_noalloc(const void* q, const void* kv_pool, const int32_t* block_table,
+                              const int32_t* cache_seqlens, void* o, float* lse, int64_t B, int64_t H,
+                              int64_t d_qk, int64_t d_v, int64_t page_size, int64_t num_pages,
+                              int64_t max_pages_per_seq, int64_t q_sb, int64_t q_sh, int64_t kv_sp,
+                              int64_t kv_ss, int64_t bt_sb, int64_t o_sb, int64_t o_sh,
+                              float softmax_scale, dmla_stream_t stream);
+
+/*
  * Decode tile-scheduler plan, computed on the device from cache_seqlens (no reference
  * counterpart; the step between the block table and the decode kernel).  The 32-token key
  * tiles of all sequences, in order, are cut into R ranges (R = CUs / head groups of 64 heads,
