@@ -96,6 +96,19 @@ __device__ __forceinline__ void dma16_after(const void* sbase, unsigned voff, un
                : "s"(sl), "v"(voff), "s"(reinterpret_cast<const void*>(sb)), "v"(d0), "v"(d1), "v"(d2), "v"(d3)
                : "m0");
 }
+// The same ordered after LDS reads whose results are d0..d3 (here: MFMA operands read from the
+// slot being refilled): as asm inputs they make the compiler wait for those reads first.
+__device__ __forceinline__ void dma16_after_v(const void* sbase, unsigned voff, unsigned lds_addr, const bf16x8& d0,
+                                              const bf16x8& d1, const bf16x8& d2, const bf16x8& d3) {
+  const uint64_t base = reinterpret_cast<uint64_t>(sbase);
+  const uint64_t sb = ((uint64_t)__builtin_amdgcn_readfirstlane((unsigned)(base >> 32)) << 32) |
+                      (unsigned)__builtin_amdgcn_readfirstlane((unsigned)base);
+  const unsigned sl = __builtin_amdgcn_readfirstlane(lds_addr);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(sl), "v"(voff), "s"(reinterpret_cast<const void*>(sb)), "v"(d0), "v"(d1), "v"(d2), "v"(d3)
+               : "m0");
+}
 // A 4-byte global -> LDS load per lane (lane l writes lds_addr + 4 l): used to pull lines into
 // L2 ahead of their real copies; the LDS bytes written are a scratch area nobody reads.
 __device__ __forceinline__ void dma4_addr(const void* gaddr, unsigned lds_addr) {

@@ -52,8 +52,8 @@ constexpr int kXBytes = kWaves * 1024;              // partial-score exchange, o
 constexpr int kPBytes = 4 * 1024;                   // P of the 64 rows as MFMA B operands
 constexpr int kMaxSegPages = 128;                   // page indices of a decode segment: two VGPRs
 constexpr int kXOffset = kRing * kTileBytes;
-constexpr int kPOffset = kXOffset + 2 * kXBytes;
-constexpr int kRowOffset = kPOffset + 2 * kPBytes;  // per-row exchange [3][2 key halves][64]
+constexpr int kPOffset = kXOffset + kRing * kXBytes;  // partial scores and P follow the ring's period
+constexpr int kRowOffset = kPOffset + kRing * kPBytes;  // per-row exchange [3][2 key halves][64]
 constexpr int kFlagOffset = kRowOffset + 3 * 2 * kRowsPerWG * 4;
 constexpr int kPageOffset = kFlagOffset + 2 * kWaves * 4;
 // Q staging at the start of a work item: the 64 rows (1152 B each, padded by one 16-byte chunk
@@ -170,7 +170,6 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   const int kh = wave & 1;             // key half of the tile: keys 16 kh .. +15
   const int rb = wave >> 1;            // own softmax rows 16 rb .. +15 (= 2 pair + kHalf)
   const int b = wk.b, row0 = wk.row0, tile_begin = wk.tile_begin, tile_end = wk.tile_end;
-  DMLA_LDS char* xbuf = lds + kXOffset;
   DMLA_LDS char* pbuf = lds + kPOffset;
   DMLA_LDS float* rowx = reinterpret_cast<DMLA_LDS float*>(lds + kRowOffset);
   DMLA_LDS int* flags = reinterpret_cast<DMLA_LDS int*>(lds + kFlagOffset);
@@ -185,7 +184,12 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
       return wk.ctx - 1;
     }
   };
-  const int own_lim = own_row < nrows ? limit_of(own_row) : -1;
+  // Rows past the last one (the tail of the last item) compute the item's first row again: its
+  // Q, its limit (the smallest of the item), output discarded; so no tile below that limit needs
+  // a mask for any row of the item.
+  const int own_lim = limit_of(own_row < nrows ? own_row : row0);
+  // First tile holding a key past some row's limit (the item's first row has the smallest).
+  const int first_mask_tile = max(limit_of(row0) + 1, 0) / kTileN;
 
   // ---- Q: the pair's 32 rows, this wave's dims half, as MFMA B operand --------------------
   // lane holds Q[row 32 pair + 16 qg + l16][288 kHalf + 32 c + 8 g .. +7]; loaded through LDS
@@ -244,28 +248,47 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
                                            (int64_t)(tile % (kPage / kTileN)) * kTileN * p.k_ss);
     }
   };
-  auto slot_addr = [&](int tile) { return lds_base + ((tile - tile_begin + kRing) % kRing) * kTileBytes; };
+  // Ring slot of tile t, relative to the item's first tile (t >= tile_begin - 1); the partial
+  // scores and P of tile t use exchange buffer slot_idx(t) of three as well.  The bulk of the
+  // loop passes these indices as compile-time constants.
+  auto slot_idx = [&](int t) { return (t - tile_begin + 2 * kRing) % kRing; };
+  auto slot_addr = [&](int tile) { return lds_base + slot_idx(tile) * kTileBytes; };
   // Copy k (0..ncopies-1) of this wave; rows past the valid range re-read row 0 of the tile
   // (finite data, masked later).
   f32x4 oacc[kDbWave][4];   // O^T[64 wave + 16 d + 4 g + i][16 qg + l16]
-  auto copy_part = [&](int k, const char* src, int valid_rows, unsigned dst, auto after_tag) {
+  bf16x8 vpre[kDbWave];     // V operands of the next PV (read one iteration ahead)
+  // Lane offsets of a full tile's copies (the copy's 8 r rows go into the scalar base): two
+  // column variants, rows 8r + l/8 with r even / odd.
+  const unsigned dma_off_even = dma_lane + dma_col0;
+  const unsigned dma_off_odd = dma_lane + (dma_col0 ^ dma_col_x);
+  // check_tag: the tile may end early (the last tile of a sequence); rows past the valid range
+  // then re-read row 0 of the tile (finite data, masked later).  after_tag: the copy refills
+  // this wave's chunk group of the slot whose V operands it read last iteration into vpre;
+  // vpre as asm operands orders the copy after those reads.
+  auto copy_part = [&](int k, const char* src, int valid_rows, unsigned dst, auto after_tag, auto check_tag) {
     const int r = k < 4 ? k : dma_rope_r;
-    const unsigned col = dma_col0 ^ ((r & 1) ? dma_col_x : 0u);
-    const unsigned off = 8 * r + dma_lrow < valid_rows ? dma_lane + (unsigned)(8 * r * row_stride_bytes) + col : col;
-    const void* gsrc = k < 4 ? (const void*)(src + wave * 128) : (const void*)(src + 8 * 128);
+    const char* gbase = k < 4 ? src + wave * 128 : src + 8 * 128;
+    unsigned off;
+    if constexpr (decltype(check_tag)::value) {
+      const unsigned col = dma_col0 ^ ((r & 1) ? dma_col_x : 0u);
+      off = 8 * r + dma_lrow < valid_rows ? dma_lane + (unsigned)(8 * r * row_stride_bytes) + col : col;
+    } else {
+      gbase += (int64_t)(8 * r) * row_stride_bytes;
+      off = (r & 1) ? dma_off_odd : dma_off_even;
+    }
     const unsigned ldst = k < 4 ? dst + wave * kGroupBytes + k * 1024 : dst + 8 * kGroupBytes + dma_rope_r * 1024;
-    // After PV: oacc[d][0] consumed the V read of column block d (see dma16_after).
-    if constexpr (decltype(after_tag)::value) dma16_after(gsrc, off, ldst, oacc[0][0], oacc[1][0], oacc[2][0], oacc[3][0]);
-    else dma16(gsrc, off, ldst);
+    if constexpr (decltype(after_tag)::value) dma16_after_v(gbase, off, ldst, vpre[0], vpre[1], vpre[2], vpre[3]);
+    else dma16(gbase, off, ldst);
   };
   using Plain = std::integral_constant<bool, false>;
+  using Checked = std::integral_constant<bool, true>;
   auto stage = [&](int tile, int slot_tile) {
     int valid_rows;
     const char* src = tile_src(tile, valid_rows);
     const unsigned dst = slot_addr(slot_tile);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) copy_part(k, src, valid_rows, dst, Plain{});
-    if (ncopies > 4) copy_part(4, src, valid_rows, dst, Plain{});
+    for (int k = 0; k < 4; ++k) copy_part(k, src, valid_rows, dst, Plain{}, Checked{});
+    if (ncopies > 4) copy_part(4, src, valid_rows, dst, Plain{}, Checked{});
   };
 
   // ---- per-lane LDS byte offsets -----------------------------------------------------------
@@ -288,8 +311,16 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   const int x_post = wave * 1024 + lane * 16;
   const int x_take = (wave ^ 2) * 1024 + lane * 16;
   const int p_post = rb * 1024 + lane * 16 + kh * 8;
+  // LDS address lane_off + add as one register, opaque to the compiler: the accesses through it
+  // then carry their constant parts as instruction offsets (one add per operand stream and
+  // iteration, instead of an add per access of a runtime ring slot).
+  auto lds_at = [&](int lane_off, int add) {
+    unsigned r;
+    asm("v_add_u32 %0, %1, %2" : "=v"(r) : "v"(lane_off), "s"(add));
+    return reinterpret_cast<DMLA_LDS char*>(static_cast<uintptr_t>(r));
+  };
+  const int lds0 = (int)lds_base;
 
-  auto slot_of = [&](int t) { return lds + ((t - tile_begin + kRing) % kRing) * kTileBytes; };
 
   float mref;               // max the accumulators of the own rows are relative to
   float mtrue;              // exact running max of this lane's keys of its own row
@@ -301,47 +332,47 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   // The V operands of a tile are read one iteration ahead of its PV (vload), off the burst
   // of P reads that follows each barrier; a slot's data is complete from the barrier after
   // its copies landed until this wave's next copies into it.
-  bf16x8 vpre[kDbWave];
-  auto vload = [&](int tp) {
-    const DMLA_LDS char* tb = slot_of(tp);
+  auto vload = [&](int slot) {
 #pragma unroll
     for (int d = 0; d < kDbWave; ++d) {
-      const bf16x4 v0 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tb + v_off[d]));
-      const bf16x4 v1 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tb + v_off[d] + 16 * 128));
+      const DMLA_LDS char* vb = lds_at(v_off[d], lds0 + slot * kTileBytes);
+      const bf16x4 v0 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(vb));
+      const bf16x4 v1 = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(vb + 16 * 128));
       vpre[d] = concat(v0, v1);
     }
   };
-  auto pv = [&](int tp) {
-    const DMLA_LDS char* pb = pbuf + (tp & 1) * kPBytes;
+  auto pv = [&](int buf) {
+    const DMLA_LDS char* pb = lds_at(lane * 16, lds0 + kPOffset + buf * kPBytes);
     bf16x8 pall[4];
 #pragma unroll
-    for (int qg = 0; qg < 4; ++qg) pall[qg] = *reinterpret_cast<const DMLA_LDS bf16x8*>(pb + qg * 1024 + lane * 16);
+    for (int qg = 0; qg < 4; ++qg) pall[qg] = *reinterpret_cast<const DMLA_LDS bf16x8*>(pb + qg * 1024);
 #pragma unroll
     for (int d = 0; d < kDbWave; ++d)
 #pragma unroll
       for (int qg = 0; qg < 4; ++qg) oacc[d][qg] = mfma_bf16(vpre[d], pall[qg], oacc[d][qg]);
   };
-  // Partial S^T[key 16 kh + 4g + i][pair row 16 qg + l16] of tile tq over this wave's dims
-  // half; the copies of tile `ctile` into its ring slot are issued between the k-steps.
-  // kCopy: 0 for the last two tiles of a work item (there is no tile t+2 to fetch); 1 copies
-  // into a slot nobody has read since the last barrier; 2 refills the slot this wave's PV just
-  // read, ordered after those reads by register dependences (no wait for other LDS reads, so
-  // the K reads can run ahead of it).
-  auto qk = [&](int tq, f32x4 (&sacc)[2], int ctile, auto copy_tag) {
+  // Partial S^T[key 16 kh + 4g + i][pair row 16 qg + l16] of the tile in ring slot q_slot over
+  // this wave's dims half; the copies of tile `ctile` into slot c_slot are issued between the
+  // k-steps.  kCopy: 0 for the last two tiles of a work item (there is no tile t+2 to fetch);
+  // 1 copies into a slot nobody has read since the last barrier; 2 refills this wave's chunk
+  // group of the slot whose V operands it read last iteration (ordered after those reads by
+  // register dependences, so the K reads can run ahead of it).
+  auto qk = [&](int q_slot, f32x4 (&sacc)[2], int ctile, int c_slot, auto copy_tag, auto check_tag) {
     constexpr int kCopy = decltype(copy_tag)::value;
-    const DMLA_LDS char* tb = slot_of(tq);
+    const DMLA_LDS char* kb0 = lds_at(k_off[0], lds0 + q_slot * kTileBytes);
+    const DMLA_LDS char* kb1 = lds_at(k_off[1], lds0 + q_slot * kTileBytes);
     int valid_rows = 0;
     const char* src = nullptr;
     unsigned dst = 0;
     if constexpr (kCopy) {
       src = tile_src(ctile, valid_rows);
-      dst = slot_addr(ctile);
+      dst = lds_base + c_slot * kTileBytes;
     }
     sacc[0] = sacc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
     // K operands are read two k-steps ahead of their MFMAs.
     auto kread = [&](int c) {
       const int cc = kHalf * kKcHalf + c;
-      return lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(tb + k_off[cc & 1] + (cc >> 1) * kGroupBytes));
+      return lds_read_b128(reinterpret_cast<const DMLA_LDS bf16x8*>(((cc & 1) ? kb1 : kb0) + (cc >> 1) * kGroupBytes));
     };
     bf16x8 kb[3];
     kb[0] = kread(0);
@@ -354,14 +385,14 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
       sacc[1] = mfma_bf16(a, qreg[1][c], sacc[1]);
       if constexpr (kCopy != 0) {
         using Tag = std::integral_constant<bool, kCopy == 2>;
-        if (c < 4) copy_part(c, src, valid_rows, dst, Tag{});
-        if (c == 4 && ncopies > 4) copy_part(4, src, valid_rows, dst, Tag{});
+        if (c < 4) copy_part(c, src, valid_rows, dst, Tag{}, check_tag);
+        if (c == 4 && ncopies > 4) copy_part(4, src, valid_rows, dst, Tag{}, check_tag);
       }
     }
   };
   using CopyOn = std::integral_constant<int, 1>;
   using CopyOff = std::integral_constant<int, 0>;
-  using CopyAfterPv = std::integral_constant<int, 2>;
+  using CopyAfterV = std::integral_constant<int, 2>;
   // Decode reads its tiles from HBM, with the copies of tile t+2 due one iteration later: each
   // iteration also pulls the 288 lines of tile t+4 into L2 with one 4-byte load per lane
   // (lane l of wave w: line (64 w + l) mod 288), so the real copy two iterations on hits L2.
@@ -380,11 +411,11 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     if constexpr (kPull) wait_vmem_but_one();
     else wait_vmem();
   };
-  auto post_partial = [&](int tq, const f32x4 (&sacc)[2]) {
-    *reinterpret_cast<DMLA_LDS f32x4*>(xbuf + (tq & 1) * kXBytes + x_post) = sacc[1 - kHalf];
+  auto post_partial = [&](int buf, const f32x4 (&sacc)[2]) {
+    *reinterpret_cast<DMLA_LDS f32x4*>(lds_at(x_post, lds0 + kXOffset + buf * kXBytes)) = sacc[1 - kHalf];
   };
-  auto take_scores = [&](int tq, const f32x4 (&sacc)[2]) {
-    return sacc[kHalf] + *reinterpret_cast<const DMLA_LDS f32x4*>(xbuf + (tq & 1) * kXBytes + x_take);
+  auto take_scores = [&](int buf, const f32x4 (&sacc)[2]) {
+    return sacc[kHalf] + *reinterpret_cast<const DMLA_LDS f32x4*>(lds_at(x_take, lds0 + kXOffset + buf * kXBytes));
   };
   auto masked = [&](int tq, const f32x4& s, float (&sr)[4]) {
     const int key0 = tq * kTileN + 16 * kh + 4 * g;
@@ -430,7 +461,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
       const int k = i * 64 + lane;
       const int rl = k / (kQRowBytes / 16), ch = k - rl * (kQRowBytes / 16);
       const int rq = row0 + rl;
-      const int r = rq < nrows ? rq : 0;
+      const int r = rq < nrows ? rq : row0;
       const bf16* qrow;
       if constexpr (!kDecode) {
         const int pos = r / p.H, head = r - pos * p.H;
@@ -459,12 +490,12 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
       for (int t = tile_begin; t < tile_end; ++t) {
         wait_vmem();
         __syncthreads();
-        if (t + 1 < tile_end) qk(t, sacc, t + 1, CopyOn{});
-        else qk(t, sacc, t + 1, CopyOff{});
-        post_partial(t, sacc);
+        if (t + 1 < tile_end) qk(slot_idx(t), sacc, t + 1, slot_idx(t + 1), CopyOn{}, Checked{});
+        else qk(slot_idx(t), sacc, t + 1, slot_idx(t + 1), CopyOff{}, Checked{});
+        post_partial(slot_idx(t), sacc);
         __syncthreads();
         float sr[4];
-        masked(t, take_scores(t, sacc), sr);
+        masked(t, take_scores(slot_idx(t), sacc), sr);
         mx = fmaxf(mx, fmaxf(fmaxf(sr[0], sr[1]), fmaxf(sr[2], sr[3])) * scale_log2);
       }
       wait_vmem();
@@ -479,50 +510,62 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     // the first tile of its work item).
 #pragma unroll
     for (int d = 0; d < kDbWave; ++d) vpre[d] = bf16x8{};
-    *reinterpret_cast<DMLA_LDS bf16x4*>(pbuf + ((tile_begin - 1) & 1) * kPBytes + p_post) = bf16x4{0.f, 0.f, 0.f, 0.f};
+    *reinterpret_cast<DMLA_LDS bf16x4*>(pbuf + slot_idx(tile_begin - 1) * kPBytes + p_post) = bf16x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (kExact) {
       stage(tile_begin, tile_begin);
       wait_vmem();
       __syncthreads();
     }
-    if (tile_begin + 1 < tile_end) qk(tile_begin, sacc, tile_begin + 1, CopyOn{});
-    else qk(tile_begin, sacc, tile_begin + 1, CopyOff{});
+    if (tile_begin + 1 < tile_end) qk(0, sacc, tile_begin + 1, 1, CopyOn{}, Checked{});
+    else qk(0, sacc, tile_begin + 1, 1, CopyOff{}, Checked{});
     pull(tile_begin + 3);
-    post_partial(tile_begin, sacc);
+    post_partial(0, sacc);
     if constexpr (!kExact) {
       __syncthreads();
       float sr[4];
-      masked(tile_begin, take_scores(tile_begin, sacc), sr);
+      masked(tile_begin, take_scores(0, sacc), sr);
       const float mhalf = group_max(fmaxf(fmaxf(sr[0], sr[1]), fmaxf(sr[2], sr[3])) * scale_log2);
       mref = row_max_both_halves(mhalf, 0);
     } else {
       mref = mref_init;
     }
 
-    // Iteration t: PV(t-1) and the partial scores of tile t+1 on the matrix cores with
-    // softmax(t) in between, then P(t) and the partials of t+1 are posted.  One barrier per
-    // tile.  Ring: PV reads slot(t-1), QK reads slot(t+1), slot(t) waits for PV(t), and each
-    // wave refills its own part of slot(t-1) with tile t+2 after its PV.  kKind 0 is the
-    // steady state; the last two iterations are peeled: kKind 1 fetches no tile t+2 and
-    // kKind 2 (the last tile) computes no scores for a tile t+1.  An overflow of the reference
-    // max is only recorded per lane here and acted on once, after the last tile: inputs that
-    // trigger it are rare, and a per-tile exchange of flags would cost every tile LDS traffic.
-    auto iteration = [&](int t, auto kind_tag) {
+    // Iteration t: the partial scores of tile t+1 and PV(t-1) on the matrix cores with softmax(t)
+    // in between, then P(t) and the partials of t+1 are posted.  One barrier per tile.  Ring:
+    // QK reads slot(t+1), PV(t-1) uses the V operands of slot(t-1) read last iteration, slot(t)
+    // is read for the next PV, and each wave refills its own part of slot(t-1) with tile t+2.
+    // kKind 0 is the steady state; the last two iterations are peeled: kKind 1 fetches no tile
+    // t+2 and kKind 2 (the last tile) computes no scores for a tile t+1.  kPh >= 0 passes t's
+    // ring phase (t - tile_begin) % 3 as a constant, so that every LDS address is a register
+    // plus an instruction offset; kMask: some row's causal or length limit falls inside tile t;
+    // kCheck: tile t+2 may be the item's partial last tile.  QK comes first so that its partials
+    // are ready long before they are posted.  An overflow of the reference max is only
+    // recorded per lane here and acted on once, after the last tile: inputs that trigger it are
+    // rare, and a per-tile exchange of flags would cost every tile LDS traffic.
+    auto iteration = [&](int t, auto kind_tag, auto phase_tag, auto mask_tag, auto check_tag) {
       constexpr int kKind = decltype(kind_tag)::value;
+      constexpr int kPh = decltype(phase_tag)::value;
+      const int s_cur = kPh >= 0 ? kPh : (t - tile_begin) % kRing;
+      const int s_next = s_cur == kRing - 1 ? 0 : s_cur + 1, s_prev = s_cur == 0 ? kRing - 1 : s_cur - 1;
       wait_tile();       // this wave's copies of tile t+1 have landed
       __syncthreads();   // partials(t) and P(t-1) posted; tile t+1 complete
-      const f32x4 s = take_scores(t, sacc);
-      pv(t - 1);
+      const f32x4 s = take_scores(s_cur, sacc);
       if constexpr (kKind == 0) {
-        qk(t + 1, sacc, t + 2, CopyAfterPv{});
+        qk(s_next, sacc, t + 2, s_prev, CopyAfterV{}, check_tag);
         pull(t + 4);
       }
-      if constexpr (kKind == 1) qk(t + 1, sacc, t + 2, CopyOff{});
-      vload(t);
+      if constexpr (kKind == 1) qk(s_next, sacc, t + 2, s_prev, CopyOff{}, check_tag);
+      pv(s_prev);
+      vload(s_cur);
 
       // ---- softmax of the own 16 rows x 16 keys (exp2 domain) ------------------------------
       float sr[4];
-      masked(t, s, sr);
+      if constexpr (decltype(mask_tag)::value) {
+        masked(t, s, sr);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sr[i] = s[i];
+      }
       const float mloc = fmaxf(fmaxf(sr[0], sr[1]), fmaxf(sr[2], sr[3])) * scale_log2;  // scale > 0
       mtrue = fmaxf(mtrue, mloc);
       overflow = overflow || mloc > mref + kHeadroom;
@@ -534,16 +577,28 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
         lsum += pj;
         pk[j] = (bf16)pj;
       }
-      *reinterpret_cast<DMLA_LDS bf16x4*>(pbuf + (t & 1) * kPBytes + p_post) = pk;
+      *reinterpret_cast<DMLA_LDS bf16x4*>(lds_at(p_post, lds0 + kPOffset + s_cur * kPBytes)) = pk;
       if constexpr (kKind != 2) {
-        post_partial(t + 1, sacc);
+        post_partial(s_next, sacc);
         iteration_schedule();
       }
     };
+    using K0 = std::integral_constant<int, 0>;
+    using K1 = std::integral_constant<int, 1>;
+    using K2 = std::integral_constant<int, 2>;
+    using PhRt = std::integral_constant<int, -1>;
+    using Mask = std::true_type;
+    using NoMask = std::false_type;
     int t = tile_begin;
-    for (; t + 2 < tile_end; ++t) iteration(t, std::integral_constant<int, 0>{});
-    if (t + 1 < tile_end) iteration(t++, std::integral_constant<int, 1>{});
-    iteration(t, std::integral_constant<int, 2>{});
+    if constexpr (!kExact) {
+      // The bulk: tiles below every row's limit, whose copies fetch full tiles.  The remaining
+      // tiles take the general iteration.
+      const int fast_end = min(first_mask_tile, tile_end - 3);
+      for (; t < fast_end; ++t) iteration(t, K0{}, PhRt{}, NoMask{}, Plain{});
+    }
+    for (; t + 2 < tile_end; ++t) iteration(t, K0{}, PhRt{}, Mask{}, Checked{});
+    if (t + 1 < tile_end) iteration(t++, K1{}, PhRt{}, Mask{}, Checked{});
+    iteration(t, K2{}, PhRt{}, Mask{}, Checked{});
     post_row_stats();
     if constexpr (!kExact) flags[wave] = __any(overflow) ? 1 : 0;
     wait_vmem();
@@ -558,7 +613,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
         return;
       }
     }
-    pv(tile_end - 1);
+    pv(slot_idx(tile_end - 1));
   } else {
     post_row_stats();
     __syncthreads();
