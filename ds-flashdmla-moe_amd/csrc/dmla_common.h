@@ -214,7 +214,11 @@ __device__ __forceinline__ float group_sum(float v) {
 
 // Wait until every outstanding vector-memory op of this wave (including LDS DMA) has landed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); /* gfx9 encoding: vmcnt(0) expcnt(7) lgkmcnt(15) */ }
-// All but the most recent vector-memory load done (loads retire in issue order).
-__device__ __forceinline__ void wait_vmem_but_one() { __builtin_amdgcn_s_waitcnt(0x0f71); /* vmcnt(1) */ }
+// At most N vector-memory loads of this wave outstanding (loads retire in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vmem_le() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | N);
+}
 
 }  // namespace dmla

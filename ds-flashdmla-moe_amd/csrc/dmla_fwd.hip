@@ -64,8 +64,7 @@ constexpr int kQRowBytes = kDqk * 2 + 16;
 constexpr int kQChunks = kRowsPerWG * kQRowBytes / 16;   // 4672 16-byte chunks, 73 per row
 constexpr int kQOffset = kTileBytes;
 static_assert(kQOffset + kRowsPerWG * kQRowBytes <= kXOffset + kXBytes, "Q staging fits before buffer 1");
-constexpr int kTouchOffset = kPageOffset;   // 256 B written by decode's L2 pulls
-constexpr int kLdsBytes = kTouchOffset + 256;
+constexpr int kLdsBytes = kPageOffset;
 constexpr float kHeadroom = 32.0f;                  // log2 headroom of p over the reference max
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 static_assert(kPage % kTileN == 0, "a page holds whole tiles");
@@ -353,10 +352,10 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   };
   // Partial S^T[key 16 kh + 4g + i][pair row 16 qg + l16] of the tile in ring slot q_slot over
   // this wave's dims half; the copies of tile `ctile` into slot c_slot are issued between the
-  // k-steps.  kCopy: 0 for the last two tiles of a work item (there is no tile t+2 to fetch);
-  // 1 copies into a slot nobody has read since the last barrier; 2 refills this wave's chunk
-  // group of the slot whose V operands it read last iteration (ordered after those reads by
-  // register dependences, so the K reads can run ahead of it).
+  // k-steps.  kCopy: 0 when there is no tile to fetch; 1 copies into a slot nobody has read
+  // since the last barrier; 2 refills this wave's chunk group of the slot whose V operands it
+  // has just read into vpre (ordered after those reads by register dependences, so the K reads
+  // can run ahead of it).
   auto qk = [&](int q_slot, f32x4 (&sacc)[2], int ctile, int c_slot, auto copy_tag, auto check_tag) {
     constexpr int kCopy = decltype(copy_tag)::value;
     const DMLA_LDS char* kb0 = lds_at(k_off[0], lds0 + q_slot * kTileBytes);
@@ -392,25 +391,21 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   };
   using CopyOn = std::integral_constant<int, 1>;
   using CopyOff = std::integral_constant<int, 0>;
+  // Copy distance.  Decode streams its tiles from HBM, so its copies run three tiles ahead:
+  // iteration t refills this wave's part of slot(t) with tile t+3 between the k-steps of
+  // QK(t+1), once its V operands of tile t are read (the other waves read that part of no slot,
+  // and every wave's K reads of tile t were done an iteration earlier); a tile's copies then
+  // have two iterations to land.  The prefill's tiles come from L2: its copies run two tiles
+  // ahead, into slot(t-1) during QK(t+1), which it runs before PV(t-1).  At the start of
+  // iteration t a wave waits for its copies of tile t+1; in decode those of tile t+2, its newest
+  // batch of ncopies instructions, stay in flight when they exist.
+  constexpr int kAhead = kDecode ? 3 : 2;
+  auto wait_tile = [&](bool newer_batch) {
+    if (!newer_batch) wait_vmem();
+    else if (ncopies > 4) wait_vmem_le<5>();
+    else wait_vmem_le<4>();
+  };
   using CopyAfterV = std::integral_constant<int, 2>;
-  // Decode reads its tiles from HBM, with the copies of tile t+2 due one iteration later: each
-  // iteration also pulls the 288 lines of tile t+4 into L2 with one 4-byte load per lane
-  // (lane l of wave w: line (64 w + l) mod 288), so the real copy two iterations on hits L2.
-  // Every step that issues copies ends with exactly one such load, and the waits for a tile's
-  // copies leave the newest load outstanding (wait_tile); the prefill's tiles are L2-resident.
-  constexpr bool kPull = kDecode && !kExact;
-  auto pull = [&](int tile) {
-    if constexpr (kPull) {
-      int unused_rows;
-      const char* src = tile_src(tile, unused_rows);
-      const int i = (64 * wave + lane) % (kTileN * kGroups);
-      dma4_addr(src + (i / kGroups) * row_stride_bytes + (i % kGroups) * 128, lds_base + kTouchOffset);
-    }
-  };
-  auto wait_tile = [&]() {
-    if constexpr (kPull) wait_vmem_but_one();
-    else wait_vmem();
-  };
   auto post_partial = [&](int buf, const f32x4 (&sacc)[2]) {
     *reinterpret_cast<DMLA_LDS f32x4*>(lds_at(x_post, lds0 + kXOffset + buf * kXBytes)) = sacc[1 - kHalf];
   };
@@ -505,7 +500,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
 
     // Prologue: the V operands of a tile t0-1 are zero and P(t0-1) = 0, so the PV of the first
     // iteration adds nothing; slot(t0) holds t0 (restaged after the exact path's scores pass);
-    // its partial scores are posted and the copy of t0+1 is in flight.  The fast path's
+    // its partial scores are posted and the copies of t0+1 and t0+2 are in flight.  The fast path's
     // reference max of each row is its max over tile t0 (every row with any key has one in
     // the first tile of its work item).
 #pragma unroll
@@ -518,7 +513,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     }
     if (tile_begin + 1 < tile_end) qk(0, sacc, tile_begin + 1, 1, CopyOn{}, Checked{});
     else qk(0, sacc, tile_begin + 1, 1, CopyOff{}, Checked{});
-    pull(tile_begin + 3);
+    if (kAhead == 3 && tile_begin + 2 < tile_end) stage(tile_begin + 2, tile_begin + 2);
     post_partial(0, sacc);
     if constexpr (!kExact) {
       __syncthreads();
@@ -530,33 +525,38 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
       mref = mref_init;
     }
 
-    // Iteration t: the partial scores of tile t+1 and PV(t-1) on the matrix cores with softmax(t)
+    // Iteration t: PV(t-1) and the partial scores of tile t+1 on the matrix cores with softmax(t)
     // in between, then P(t) and the partials of t+1 are posted.  One barrier per tile.  Ring:
-    // QK reads slot(t+1), PV(t-1) uses the V operands of slot(t-1) read last iteration, slot(t)
-    // is read for the next PV, and each wave refills its own part of slot(t-1) with tile t+2.
-    // kKind 0 is the steady state; the last two iterations are peeled: kKind 1 fetches no tile
-    // t+2 and kKind 2 (the last tile) computes no scores for a tile t+1.  kPh >= 0 passes t's
-    // ring phase (t - tile_begin) % 3 as a constant, so that every LDS address is a register
-    // plus an instruction offset; kMask: some row's causal or length limit falls inside tile t;
-    // kCheck: tile t+2 may be the item's partial last tile.  QK comes first so that its partials
-    // are ready long before they are posted.  An overflow of the reference max is only
-    // recorded per lane here and acted on once, after the last tile: inputs that trigger it are
-    // rare, and a per-tile exchange of flags would cost every tile LDS traffic.
+    // PV(t-1) uses the V operands read last iteration, slot(t) is read for the next PV, QK(t+1)
+    // reads slot(t+1), and the copies of tile t+kAhead go into slot(t+kAhead) (see kAhead).
+    // kKind 0 is the steady state; kKind 1 (t+kAhead past the end) copies nothing and kKind 2
+    // (the last tile) computes no scores for a tile t+1.  kPh >= 0 would pass t's ring phase as
+    // a constant (the loop below passes it at run time); kMask: some row's causal or length
+    // limit falls inside tile t; kCheck: tile t+kAhead may be the item's partial last tile.  An
+    // overflow of the reference max is only recorded per lane here and acted on once, after the
+    // last tile: inputs that trigger it are rare, and a per-tile exchange of flags would cost
+    // every tile LDS traffic.
     auto iteration = [&](int t, auto kind_tag, auto phase_tag, auto mask_tag, auto check_tag) {
       constexpr int kKind = decltype(kind_tag)::value;
       constexpr int kPh = decltype(phase_tag)::value;
       const int s_cur = kPh >= 0 ? kPh : (t - tile_begin) % kRing;
       const int s_next = s_cur == kRing - 1 ? 0 : s_cur + 1, s_prev = s_cur == 0 ? kRing - 1 : s_cur - 1;
-      wait_tile();       // this wave's copies of tile t+1 have landed
+      wait_tile(kAhead == 3 && t + 2 < tile_end);   // this wave's copies of tile t+1 have landed
       __syncthreads();   // partials(t) and P(t-1) posted; tile t+1 complete
       const f32x4 s = take_scores(s_cur, sacc);
-      if constexpr (kKind == 0) {
-        qk(s_next, sacc, t + 2, s_prev, CopyAfterV{}, check_tag);
-        pull(t + 4);
+      if constexpr (kAhead == 3) {
+        pv(s_prev);
+        vload(s_cur);
+        if constexpr (kKind == 0) qk(s_next, sacc, t + 3, s_cur, CopyAfterV{}, check_tag);
+        if constexpr (kKind == 1) qk(s_next, sacc, 0, 0, CopyOff{}, check_tag);
+      } else {
+        // QK first, so that its partials are ready long before they are posted (vpre still
+        // holds the V operands of slot(t-1), the slot refilled here)
+        if constexpr (kKind == 0) qk(s_next, sacc, t + 2, s_prev, CopyAfterV{}, check_tag);
+        if constexpr (kKind == 1) qk(s_next, sacc, 0, 0, CopyOff{}, check_tag);
+        pv(s_prev);
+        vload(s_cur);
       }
-      if constexpr (kKind == 1) qk(s_next, sacc, t + 2, s_prev, CopyOff{}, check_tag);
-      pv(s_prev);
-      vload(s_cur);
 
       // ---- softmax of the own 16 rows x 16 keys (exp2 domain) ------------------------------
       float sr[4];
@@ -593,11 +593,11 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
     if constexpr (!kExact) {
       // The bulk: tiles below every row's limit, whose copies fetch full tiles.  The remaining
       // tiles take the general iteration.
-      const int fast_end = min(first_mask_tile, tile_end - 3);
+      const int fast_end = min(first_mask_tile, tile_end - kAhead - 1);
       for (; t < fast_end; ++t) iteration(t, K0{}, PhRt{}, NoMask{}, Plain{});
     }
-    for (; t + 2 < tile_end; ++t) iteration(t, K0{}, PhRt{}, Mask{}, Checked{});
-    if (t + 1 < tile_end) iteration(t++, K1{}, PhRt{}, Mask{}, Checked{});
+    for (; t + kAhead < tile_end; ++t) iteration(t, K0{}, PhRt{}, Mask{}, Checked{});
+    for (; t + 1 < tile_end; ++t) iteration(t, K1{}, PhRt{}, Mask{}, Checked{});
     iteration(t, K2{}, PhRt{}, Mask{}, Checked{});
     post_row_stats();
     if constexpr (!kExact) flags[wave] = __any(overflow) ? 1 : 0;
