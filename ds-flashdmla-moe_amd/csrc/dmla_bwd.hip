@@ -19,12 +19,22 @@
 //   bwd_dk_reduce_kernel  sums the dK_lat partials of the row segments in a fixed order.
 // No atomics anywhere: the result is bitwise deterministic.
 //
+// dS' is stored only where it is written: for each 128-row group, the 64-key blocks that some
+// of its rows can see (a prefix of the key blocks; all of them without a causal mask), packed
+// group after group through an offset table (bwd_prep_kernel builds it).  When that storage
+// would pass DMLA_BWD_DS_CAP_BYTES, the rows are cut into chunks of whole groups, each run
+// through dK/dV, dQ and the reduction in turn: a chunk's dQ rows are complete, and dK_lat
+// accumulates over the chunks in fp32 (the fp32 output itself, or a workspace buffer when dK_lat
+// is bf16), so the workspace stays bounded whatever S is.
+//
 // Operand precision: S = Q K^T and dP = dO V^T multiply the bf16 inputs as they are.  The
 // second-stage products dS'^T Q, P^T dO and dS' K take fp16 operands: P and dS' are rounded to
 // fp16 (11-bit significand) instead of bf16 (8-bit), and Q, dO, K_lat are converted to fp16
 // exactly.  A key that every later row of every head attends to sums thousands of such terms;
 // with bf16 P and dS' that rounding alone costs ~1e-3 of |dK_lat| (2e-2 at the config-5
 // magnitudes of ~20), with fp16 an eighth of it -- within a few 1e-3 of exact fp32 operands.
+#include <cstdlib>
+
 #include "dmla_common.h"
 #include "dmla_host.h"
 
@@ -73,36 +83,56 @@ struct BwdParams {
   int n_rt;             // 32-row tiles per batch element, even: 2 * ceil(R / 64)
   int n_kb;             // 64-key blocks: ceil(Sk / 64)
   int n_pairs;          // ceil(n_kb / 2)
-  int parts;            // row segments per key-block pair
+  int parts;            // row segments per key-block pair (this chunk)
   int n_items;          // B * n_pairs * parts
   int kt_ld;            // K^T row length (keys): 64 * n_kb
+  int n_groups;         // 128-row groups: ceil(n_rt / 4)
+  int rt_begin, rt_end; // this chunk's row tiles (group aligned)
+  int chunk_pairs;      // (group, 64-key block) pairs of this chunk: dS' blocks per batch element
+  int chunk, last_chunk;
   float2* lsed;         // [B][32 n_rt] (lse2, D); padding rows hold (+inf, 0)
   _Float16* kt;         // [B][576][kt_ld] fp16
-  _Float16* ds;         // [B][2 n_rt row blocks][4 n_kb key blocks][256]: fp16 dS' 16x16 blocks, MFMA C order
+  int32_t* goff;        // [n_groups + 1]: first (group, key block) pair of each group
+  _Float16* ds;         // [B][chunk_pairs][8 row blocks][4 key blocks][256]: fp16 dS' 16x16 blocks, MFMA C order
   float* part;          // [n_items][2][4 kb][36 cb][64 lanes][4]: dK_lat partials in MFMA C order
+  float* dk_acc;        // fp32 dK_lat of the chunks so far: [B][Sk][576], or the fp32 output itself
 };
 
 // ---- work split of the dK/dV kernel, shared by the host and the reduction ------------------
 // Key block kb needs the row tiles from first_row_tile(kb) on (causal: rows whose position can
 // see key 64 kb), rounded down to a multiple of four tiles so that every 128-row dQ tile that
-// reads a dS' block of kb finds it written.  Blocks kb and n_kb-1-kb form a pair: the first is walked from
-// the last row tile down, the second from its first row tile up, so every pair has about the
-// same length and, at any moment, all pairs of a batch element read the same one or two row
-// tiles (L2 sharing).  Each pair's steps are cut into `parts` equal segments.
+// reads a dS' block of kb finds it written; within a chunk, the row tiles [rt_begin, rt_end) of
+// those.  Blocks kb and n_kb-1-kb form a pair: the first is walked from the chunk's last row
+// tile down, the second from its first row tile up, so every pair has about the same length and,
+// at any moment, all pairs of a batch element read the same one or two row tiles (L2 sharing).
+// Each pair's steps are cut into `parts` equal segments.
 __host__ __device__ inline int first_row_tile(int causal, int Sq, int Sk, int H, int kb) {
   if (!causal) return 0;
   const int first_pos = max(0, kKeys * kb - (Sk - Sq));
   return 4 * (int)(((int64_t)first_pos * H) / 128);
 }
+// 64-key blocks that write dS' for 128-row group t: those with first_row_tile <= 4 t, a prefix
+// of the key blocks since first_row_tile does not decrease.
+__host__ __device__ inline int group_key_blocks(int causal, int Sq, int Sk, int H, int n_kb, int t) {
+  int lo = 0, hi = n_kb;   // first kb with first_row_tile(kb) > 4 t
+  while (lo < hi) {
+    const int mid = (lo + hi) / 2;
+    if (first_row_tile(causal, Sq, Sk, H, mid) <= 4 * t) lo = mid + 1; else hi = mid;
+  }
+  return lo;
+}
 struct PairPlan {
-  int kb_a, kb_b, steps_a, total;
+  int kb_a, kb_b, first_a, first_b, steps_a, total;
 };
-__host__ __device__ inline PairPlan pair_plan(int causal, int Sq, int Sk, int H, int n_rt, int n_kb, int i) {
+__host__ __device__ inline PairPlan pair_plan(int causal, int Sq, int Sk, int H, int rt_begin, int rt_end, int n_kb,
+                                              int i) {
   PairPlan pp;
   pp.kb_a = i;
   pp.kb_b = n_kb - 1 - i;
-  pp.steps_a = n_rt - first_row_tile(causal, Sq, Sk, H, pp.kb_a);
-  pp.total = pp.steps_a + (pp.kb_b != pp.kb_a ? n_rt - first_row_tile(causal, Sq, Sk, H, pp.kb_b) : 0);
+  pp.first_a = max(rt_begin, first_row_tile(causal, Sq, Sk, H, pp.kb_a));
+  pp.first_b = max(rt_begin, first_row_tile(causal, Sq, Sk, H, pp.kb_b));
+  pp.steps_a = max(0, rt_end - pp.first_a);
+  pp.total = pp.steps_a + (pp.kb_b != pp.kb_a ? max(0, rt_end - pp.first_b) : 0);
   return pp;
 }
 __host__ __device__ inline int part_begin(int total, int parts, int j) {
@@ -122,6 +152,30 @@ __device__ __forceinline__ f16x4 to_f16x4(float a, float b, float c, float d) {
 __global__ void __launch_bounds__(256) bwd_prep_kernel(BwdParams p) {
   const int b = blockIdx.y;
   const int t = threadIdx.x;
+  if (blockIdx.x == 0 && blockIdx.y == 0) {
+    // goff: exclusive prefix of group_key_blocks over the groups, 256 groups per round (a
+    // shuffle scan per wave, the four wave totals through LDS).
+    __shared__ int wsum[4];
+    int carry = 0;
+    for (int base = 0; base <= p.n_groups; base += 256) {
+      const int gi = base + t;
+      const int v = gi < p.n_groups ? group_key_blocks(p.causal, p.Sq, p.Sk, p.H, p.n_kb, gi) : 0;
+      int x = v;
+      const int ln = t & 63, wv = t >> 6;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (ln >= o) x += y;
+      }
+      if (ln == 63) wsum[wv] = x;
+      __syncthreads();
+      int before = carry;
+      for (int w = 0; w < wv; ++w) before += wsum[w];
+      if (gi <= p.n_groups) p.goff[gi] = before + x - v;
+      carry += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+      __syncthreads();
+    }
+  }
   const int row = blockIdx.x * kRows + (t >> 3);
   const int part = t & 7;
   float dsum = 0.f;
@@ -227,8 +281,9 @@ bwd_dkdv_kernel(BwdParams p) {
   const int pi = u % p.n_pairs;
   const int pj = (u / p.n_pairs) % p.parts;
   const int b = u / (p.n_pairs * p.parts);
-  const PairPlan pp = pair_plan(p.causal, p.Sq, p.Sk, p.H, p.n_rt, p.n_kb, pi);
+  const PairPlan pp = pair_plan(p.causal, p.Sq, p.Sk, p.H, p.rt_begin, p.rt_end, p.n_kb, pi);
   const int lo = part_begin(pp.total, p.parts, pj), hi = part_begin(pp.total, p.parts, pj + 1);
+  const int goff0 = p.goff[p.rt_begin / 4];
 
   const int l16 = lane & 15, g = lane >> 4;
   const int rb = wave >> 1;      // S-phase row block
@@ -262,8 +317,7 @@ bwd_dkdv_kernel(BwdParams p) {
     const int count = g_hi - g_lo;
     const int kb = ph == 0 ? pp.kb_a : pp.kb_b;
     const int dir = ph == 0 ? -1 : 1;
-    const int rt_first = ph == 0 ? p.n_rt - 1 - g_lo
-                                 : first_row_tile(p.causal, p.Sq, p.Sk, p.H, kb) + (g_lo - pp.steps_a);
+    const int rt_first = ph == 0 ? p.rt_end - 1 - g_lo : pp.first_b + (g_lo - pp.steps_a);
     if (!first_segment) __syncthreads();   // the previous segment's last tile is still being read
     first_segment = false;
     const int key0 = kb * kKeys;
@@ -314,10 +368,14 @@ bwd_dkdv_kernel(BwdParams p) {
       if (i < kQGroups) dma16_addr(qsrc + 128 * i, cdst + i * kGroupBytes);
       else dma16_addr(osrc + 128 * (i - kQGroups), cdst + kQBytes + (i - kQGroups) * kGroupBytes);
     };
-    // (lse2, D) and key limit of this lane's 4 rows 32 rt + 16 rb + 4 g + i.
+    // (lse2, D) and key limit of this lane's 4 rows 32 rt + 16 rb + 4 g + i, and the dS' pair of
+    // (rt's group, kb).  Loaded one tile ahead, with the statistics: a load issued after the
+    // tile's copies would wait for all of them (vector-memory loads complete in order).
     float lse2[4], dval[4];
     int lim[4];
+    int64_t ds_pair = 0;
     auto row_stats = [&](int rt) {
+      ds_pair = (int64_t)b * p.chunk_pairs + p.goff[rt >> 2] - goff0 + kb;
       const int r0 = rt * kRows + 16 * rb + 4 * g;
       const float4* src = reinterpret_cast<const float4*>(p.lsed + (int64_t)b * p.n_rt * kRows + r0);
       const float4 a0 = src[0], a1 = src[1];
@@ -416,7 +474,7 @@ bwd_dkdv_kernel(BwdParams p) {
         const int kbl = 2 * dh + kk;
         *reinterpret_cast<DMLA_LDS f16x4*>(xbuf + kbl * 1024 + lane * 16 + 8 * rb) = pb;
         *reinterpret_cast<DMLA_LDS f16x4*>(xbuf + 4096 + kbl * 1024 + lane * 16 + 8 * rb) = db;
-        _Float16* dsblk = p.ds + ((((int64_t)b * 2 * p.n_rt + 2 * rt + rb) * (4 * p.n_kb)) + 4 * kb + kbl) * 256;
+        _Float16* dsblk = p.ds + ((ds_pair * 8 + 2 * (rt & 3) + rb) * 4 + kbl) * 256;
         *reinterpret_cast<f16x4*>(dsblk + 4 * lane) = db;
       }
       __syncthreads();   // exchange written
@@ -489,10 +547,10 @@ __global__ void __launch_bounds__(kDqThreads, 1) bwd_dq_kernel(BwdParams p) {
   DMLA_LDS char* lds = (DMLA_LDS char*)smem;
   const int wave = uniform(threadIdx.x >> 6);
   const int lane = lane_id();
-  const int n_t = (p.R + kDqRows - 1) / kDqRows;
-  // Heaviest (latest) row tiles first.
+  // The chunk's 128-row tiles (its row groups), heaviest (latest) first.
+  const int g_end = (p.rt_end + 3) / 4;
   const int b = (int)blockIdx.x % p.B;
-  const int t = n_t - 1 - (int)blockIdx.x / p.B;
+  const int t = g_end - 1 - (int)blockIdx.x / p.B;
   const int row0 = kDqRows * t;
   const int last_row = min(p.R, row0 + kDqRows) - 1;
   const int kmax = p.causal ? min(p.Sk - 1, last_row / p.H + (p.Sk - p.Sq)) : p.Sk - 1;
@@ -504,18 +562,19 @@ __global__ void __launch_bounds__(kDqThreads, 1) bwd_dq_kernel(BwdParams p) {
   // Row blocks of 16 that exist in the dS' buffer (rows padded to 64).
   const int n_rb = 2 * p.n_rt;
 
-  // Copies.  dS': wave w moves row block 8 t + w, key blocks 2 kt, 2 kt + 1 (1 KB contiguous).
+  // Copies.  dS': wave w moves row block w of the group, key blocks 2 kt, 2 kt + 1 (1 KB contiguous).
   // K^T: 16 dims x 32 keys per copy (1 KB), wave w copies dim blocks w, w+8, .. (5 or 4 copies);
   // lane l -> dim 16 n + l/4, physical chunk l%4 = logical chunk (l%4) ^ (l/16).
   const unsigned kt_voff = (unsigned)(((lane >> 2) * p.kt_ld + 8 * ((lane & 3) ^ (lane >> 4))) * 2);
   // Every wave issues exactly kDqCopies copies per stage (so one vmcnt value waits for a stage):
   // a row block past the buffer copies row block 0 instead (its rows are not stored), and
   // waves 4-7 copy their dim block w + 24 a second time (same bytes to the same place).
-  const int rblk = 8 * t + wave < n_rb ? 8 * t + wave : 0;
+  const int rblk = 8 * t + wave < n_rb ? wave : 0;
+  const int64_t pair0 = (int64_t)b * p.chunk_pairs + p.goff[t] - p.goff[p.rt_begin / 4];
   auto copy = [&](int kt, int st, int m) {
     const unsigned dst = lds_base + st * kDqStageBytes;
     if (m == 0) {
-      const _Float16* dsrc = p.ds + ((((int64_t)b * 2 * p.n_rt + rblk) * (4 * p.n_kb)) + 2 * kt) * 256;
+      const _Float16* dsrc = p.ds + (((pair0 + (kt >> 1)) * 8 + rblk) * 4 + 2 * (kt & 1)) * 256;
       dma16(dsrc, 16u * lane, dst + wave * 1024);
     } else {
       const int n0 = wave + 8 * (m - 1);
@@ -596,7 +655,7 @@ __global__ void __launch_bounds__(256) bwd_dk_reduce_kernel(BwdParams p) {
   const int b = blockIdx.z, kb = blockIdx.y, kbl = blockIdx.x;
   const int pi = min(kb, p.n_kb - 1 - kb);
   const int ph = kb == pi ? 0 : 1;
-  const PairPlan pp = pair_plan(p.causal, p.Sq, p.Sk, p.H, p.n_rt, p.n_kb, pi);
+  const PairPlan pp = pair_plan(p.causal, p.Sq, p.Sk, p.H, p.rt_begin, p.rt_end, p.n_kb, pi);
   const int iv_lo = ph == 0 ? 0 : pp.steps_a;
   const int iv_hi = ph == 0 ? pp.steps_a : pp.total;
   for (int idx = threadIdx.x; idx < kCb * 64; idx += 256) {
@@ -613,20 +672,72 @@ __global__ void __launch_bounds__(256) bwd_dk_reduce_kernel(BwdParams p) {
     for (int i = 0; i < 4; ++i) {
       const int key = kb * kKeys + 16 * kbl + 4 * (ln >> 4) + i;
       if (key >= p.Sk) continue;
-      const int64_t o = b * p.dk_sb + key * p.dk_ss + 16 * cb + (ln & 15);
-      if (p.dk_fp32) static_cast<float*>(p.dk)[o] = s[i];
-      else static_cast<bf16*>(p.dk)[o] = (bf16)s[i];
+      const int col = 16 * cb + (ln & 15);
+      const int64_t o = b * p.dk_sb + key * p.dk_ss + col;
+      // Chunks after the first add to the fp32 sum of the earlier ones; the last writes dK_lat.
+      const int64_t oa = p.dk_fp32 ? o : ((int64_t)b * p.Sk + key) * kDqk + col;
+      float v = s[i];
+      if (p.chunk > 0) v += p.dk_acc[oa];
+      if (!p.last_chunk) p.dk_acc[oa] = v;
+      else if (p.dk_fp32) static_cast<float*>(p.dk)[o] = v;
+      else static_cast<bf16*>(p.dk)[o] = (bf16)v;
     }
   }
 }
 
 // ---- host-side planning ----------------------------------------------------------------------
+// dS' bytes of one (128-row group, 64-key block) pair: 8 row blocks x 4 key blocks x 256 fp16.
+constexpr int64_t kPairBytes = 8 * 4 * 256 * 2;
+
+// The cap on a chunk's dS' storage: DMLA_BWD_DS_CAP_BYTES, or the environment variable of that
+// name when set (tests use it to force several chunks at small sizes).
+int64_t ds_cap_bytes() {
+  const char* e = getenv("DMLA_BWD_DS_CAP_BYTES");
+  if (e != nullptr && *e) {
+    const long long v = atoll(e);
+    if (v > 0) return v;
+  }
+  return DMLA_BWD_DS_CAP_BYTES;
+}
+
+struct BwdChunk {
+  int g0, g1;      // row groups [g0, g1)
+  int pairs;       // (group, key block) pairs: dS' blocks per batch element
+  int parts, n_items;
+};
+
 struct BwdPlan {
-  int R, n_rt, n_kb, n_pairs, parts, n_items, kt_ld;
-  int64_t off_lsed, off_kt, off_ds, off_part, bytes;
+  int R, n_rt, n_kb, n_pairs, kt_ld, n_groups;
+  int n_chunks, max_pairs, max_items;
+  int64_t off_lsed, off_kt, off_goff, off_ds, off_part, off_acc, bytes;
 };
 
 int64_t round256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+// The chunk starting at group g0: whole groups while their dS' fits the cap (at least one).
+BwdChunk next_chunk(const BwdPlan& pl, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int causal, int cus, int g0,
+                    int64_t cap) {
+  BwdChunk c = {};
+  c.g0 = g0;
+  c.g1 = g0;
+  int64_t pairs = 0;
+  while (c.g1 < pl.n_groups) {
+    const int nk = group_key_blocks(causal, (int)Sq, (int)Sk, (int)H, pl.n_kb, c.g1);
+    if (c.g1 > g0 && (pairs + nk) * B * kPairBytes > cap) break;
+    pairs += nk;
+    ++c.g1;
+  }
+  c.pairs = (int)pairs;
+  const int rt0 = 4 * c.g0, rt1 = min(pl.n_rt, 4 * c.g1);
+  int max_total = 1;
+  for (int i = 0; i < pl.n_pairs; ++i)
+    max_total = max(max_total, pair_plan(causal, (int)Sq, (int)Sk, (int)H, rt0, rt1, pl.n_kb, i).total);
+  const int64_t base = B * pl.n_pairs;
+  int parts = (int)((cus + base - 1) / base);
+  c.parts = max(1, min(parts, min(kMaxParts, max_total)));
+  c.n_items = (int)(base * c.parts);
+  return c;
+}
 
 BwdPlan make_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int causal, int cus) {
   BwdPlan pl = {};
@@ -634,20 +745,23 @@ BwdPlan make_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int causal, int 
   pl.n_rt = 2 * (int)((pl.R + 63) / 64);
   pl.n_kb = (int)((Sk + kKeys - 1) / kKeys);
   pl.n_pairs = (pl.n_kb + 1) / 2;
-  int max_total = 1;
-  for (int i = 0; i < pl.n_pairs; ++i)
-    max_total = max(max_total, pair_plan(causal, (int)Sq, (int)Sk, (int)H, pl.n_rt, pl.n_kb, i).total);
-  const int64_t base = B * pl.n_pairs;
-  int parts = (int)((cus + base - 1) / base);
-  parts = max(1, min(parts, min(kMaxParts, max_total)));
-  pl.parts = parts;
-  pl.n_items = (int)(base * parts);
   pl.kt_ld = kKeys * pl.n_kb;
+  pl.n_groups = (pl.n_rt + 3) / 4;
+  const int64_t cap = ds_cap_bytes();
+  for (int g0 = 0; g0 < pl.n_groups;) {
+    const BwdChunk c = next_chunk(pl, B, H, Sq, Sk, causal, cus, g0, cap);
+    ++pl.n_chunks;
+    pl.max_pairs = max(pl.max_pairs, c.pairs);
+    pl.max_items = max(pl.max_items, c.n_items);
+    g0 = c.g1;
+  }
   int64_t o = 0;
   pl.off_lsed = o; o += round256(B * pl.n_rt * kRows * 8);
   pl.off_kt = o;   o += round256(B * kDqk * (int64_t)pl.kt_ld * 2);
-  pl.off_ds = o;   o += round256(B * 2 * (int64_t)pl.n_rt * 4 * pl.n_kb * 512);
-  pl.off_part = o; o += round256((int64_t)pl.n_items * 2 * kPartFloats * 4);
+  pl.off_goff = o; o += round256(((int64_t)pl.n_groups + 1) * 4);
+  pl.off_ds = o;   o += round256(B * (int64_t)pl.max_pairs * kPairBytes);
+  pl.off_part = o; o += round256((int64_t)pl.max_items * 2 * kPartFloats * 4);
+  pl.off_acc = o;  o += pl.n_chunks > 1 ? round256(B * Sk * kDqk * 4) : 0;
   pl.bytes = o;
   return pl;
 }
@@ -723,22 +837,38 @@ extern "C" int dmla_bwd_cache_latent(const void* q, const void* k_lat, const voi
   p.hdiv = make_fastdiv((unsigned)H);
   p.scale = softmax_scale;
   p.scale_log2 = softmax_scale * kLog2e;
-  p.R = pl.R; p.n_rt = pl.n_rt; p.n_kb = pl.n_kb; p.n_pairs = pl.n_pairs; p.parts = pl.parts;
-  p.n_items = pl.n_items; p.kt_ld = pl.kt_ld;
+  p.R = pl.R; p.n_rt = pl.n_rt; p.n_kb = pl.n_kb; p.n_pairs = pl.n_pairs;
+  p.kt_ld = pl.kt_ld; p.n_groups = pl.n_groups;
   char* ws = static_cast<char*>(workspace);
   p.lsed = reinterpret_cast<float2*>(ws + pl.off_lsed);
   p.kt = reinterpret_cast<_Float16*>(ws + pl.off_kt);
+  p.goff = reinterpret_cast<int32_t*>(ws + pl.off_goff);
   p.ds = reinterpret_cast<_Float16*>(ws + pl.off_ds);
   p.part = reinterpret_cast<float*>(ws + pl.off_part);
+  p.dk_acc = dk_fp32 ? static_cast<float*>(dk_lat) : reinterpret_cast<float*>(ws + pl.off_acc);
+  if (B * ((int64_t)pl.n_groups) > 0x7fffffff)
+    return fail(DMLA_ERR_UNSUPPORTED, "dmla_bwd_cache_latent: grid too large");
 
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)pl.n_rt, (unsigned)B), dim3(256), 0, s, p);
   hipLaunchKernelGGL(bwd_kt_kernel, dim3(kDqk / 64, (unsigned)pl.n_kb, (unsigned)B), dim3(256), 0, s, p);
-  const int64_t grid_kv = 8 * ((pl.n_items + 7) / 8);
-  hipLaunchKernelGGL(bwd_dkdv_kernel, dim3((unsigned)grid_kv), dim3(kBwdThreads), 0, s, p);
-  const int64_t grid_q = B * ((pl.R + kDqRows - 1) / kDqRows);
-  if (grid_q > 0x7fffffff) return fail(DMLA_ERR_UNSUPPORTED, "dmla_bwd_cache_latent: grid too large");
-  hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)grid_q), dim3(kDqThreads), 0, s, p);
-  hipLaunchKernelGGL(bwd_dk_reduce_kernel, dim3(4, (unsigned)pl.n_kb, (unsigned)B), dim3(256), 0, s, p);
+  const int cus = device_cu_count();
+  const int64_t cap = ds_cap_bytes();
+  int chunk = 0;
+  for (int g0 = 0; g0 < pl.n_groups; ++chunk) {
+    const BwdChunk c = next_chunk(pl, B, H, Sq, Sk, causal ? 1 : 0, cus, g0, cap);
+    p.rt_begin = 4 * c.g0;
+    p.rt_end = min(pl.n_rt, 4 * c.g1);
+    p.chunk_pairs = c.pairs;
+    p.parts = c.parts;
+    p.n_items = c.n_items;
+    p.chunk = chunk;
+    p.last_chunk = c.g1 >= pl.n_groups ? 1 : 0;
+    const int64_t grid_kv = 8 * ((c.n_items + 7) / 8);
+    hipLaunchKernelGGL(bwd_dkdv_kernel, dim3((unsigned)grid_kv), dim3(kBwdThreads), 0, s, p);
+    hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)(B * (c.g1 - c.g0))), dim3(kDqThreads), 0, s, p);
+    hipLaunchKernelGGL(bwd_dk_reduce_kernel, dim3(4, (unsigned)pl.n_kb, (unsigned)B), dim3(256), 0, s, p);
+    g0 = c.g1;
+  }
   return check_launch("dmla_bwd_cache_latent");
 }

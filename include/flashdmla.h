@@ -243,9 +243,14 @@ int dmla_lse_combine(const float* part_o, const float* part_lse, const int32_t* 
  *   fp32.
  *   The result is deterministic (no atomics).  workspace: device memory of at least
  *   dmla_bwd_workspace_bytes(...) bytes for the same sizes on the current device, 16-byte
- *   aligned; its contents on entry do not matter.
+ *   aligned; its contents on entry do not matter.  The workspace grows linearly in Sq and Sk:
+ *   dS is kept only for the (row, key) blocks that the causal mask leaves, and when that would
+ *   pass DMLA_BWD_DS_CAP_BYTES (or the environment variable DMLA_BWD_DS_CAP_BYTES, read at
+ *   each call) the rows are processed in chunks whose dS fits it, dk_lat accumulating in fp32
+ *   across the chunks (in the workspace when dk_lat is bf16).
  * Supported: d_qk = 576, d_v = 512.
  */
+#define DMLA_BWD_DS_CAP_BYTES (512ll << 20)
 int64_t dmla_bwd_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t d_qk,
                                  int64_t d_v, int causal);
 int dmla_bwd_cache_latent(const void* q, const void* k_lat, const void* o, const void* dout,

@@ -233,3 +233,16 @@ def test_fp16_range_check_rejects_values_the_kernels_would_saturate():
 def test_onthefly_forward_wrapper_takes_check_range():
     import inspect
     assert "check_range" in inspect.signature(ops.flash_dmla_fwd_onthefly).parameters
+
+
+def test_bwd_workspace_grows_linearly_with_the_sequence():
+    # dS' storage covers only the causal blocks and is capped (row chunks past the cap), so the
+    # workspace no longer grows as S^2: ~linear terms (K^T, statistics, partials) plus the cap.
+    lib = _lib.lib()
+    ws = {S: lib.dmla_bwd_workspace_bytes(4, 16, S, S, 576, 512, 1) for S in (2048, 8192, 16384, 65536)}
+    full_square = lambda S: 4 * 16 * S * S * 2        # the former layout's dS' alone
+    assert ws[2048] < 0.75 * full_square(2048) + (200 << 20)
+    assert ws[65536] < 5 * ws[16384]                  # S^2 growth would be 16x
+    assert ws[65536] < (5 << 30) and full_square(65536) > (500 << 30)
+    non_causal = lib.dmla_bwd_workspace_bytes(4, 16, 2048, 2048, 576, 512, 0)
+    assert non_causal > ws[2048]

@@ -126,3 +126,50 @@ def test_autograd_function_matches_fp32_autograd(gpu):
     assert_out_close(qg.grad, dq_ag, "dq through autograd.Function")
     diff = (kg.grad.float().cpu() - dk_ag).abs()
     assert (diff <= 2e-2 + dk_ag.abs() * 2.0 ** -9).all(), f"dk bf16 max diff {diff.max().item():.3e}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize(
+    "B,H,Sq,Sk,causal,dk_dtype",
+    [
+        (2, 4, 600, 600, True, torch.float32),    # many chunks, dk accumulated in the fp32 output
+        (2, 4, 600, 600, True, torch.bfloat16),   # the same through the workspace accumulator
+        (1, 3, 300, 500, True, torch.float32),    # bottom-right causal, heads not dividing a tile
+        (1, 4, 200, 350, False, torch.float32),   # non-causal: every group holds every key block
+    ],
+)
+def test_bwd_row_chunks(gpu, monkeypatch, B, H, Sq, Sk, causal, dk_dtype):
+    # A 96 KB cap on dS' storage (the default is 512 MiB) cuts these rows into several chunks of
+    # 128-row groups; each chunk's dq rows are final and dk_lat sums over the chunks.
+    monkeypatch.setenv("DMLA_BWD_DS_CAP_BYTES", str(96 * 1024))
+    from python import _lib
+    small = _lib.lib().dmla_bwd_workspace_bytes(B, H, Sq, Sk, 576, 512, 1 if causal else 0)
+    q, k, do = _inputs(B, H, Sq, Sk, seed=B * 7 + H * 3 + Sq)
+    o, m, l, dq, dk = _run(gpu, q, k, do, causal, dk_dtype=dk_dtype)
+    dq_ref, dk_ref = R.dmla_bwd_cache_latent(q.float(), k.float(), o.cpu().float(), do.float(), m.cpu(), l.cpu(),
+                                             512, SCALE, causal)
+    assert_out_close(dq, dq_ref, "dq (row chunks)")
+    if dk_dtype == torch.float32:
+        assert_out_close(dk, dk_ref, "dk_lat (row chunks)")
+    else:
+        diff = (dk.float().cpu() - dk_ref).abs()
+        assert (diff <= 2e-2 + dk_ref.abs() * 2.0 ** -9).all(), f"dk bf16 max diff {diff.max().item():.3e}"
+    # the same call without the cap (one chunk) agrees to fp32 summation-order differences
+    monkeypatch.delenv("DMLA_BWD_DS_CAP_BYTES")
+    assert _lib.lib().dmla_bwd_workspace_bytes(B, H, Sq, Sk, 576, 512, 1 if causal else 0) != small
+    _, _, _, dq1, dk1 = _run(gpu, q, k, do, causal, dk_dtype=dk_dtype)
+    assert torch.equal(dq, dq1), "dq rows do not depend on the chunking"
+    # fp32 sums in another order: ~1e-6 in fp32, up to one bf16 step (2^-7 relative) in bf16
+    tol = 1e-3 + dk1.float().abs() * (2.0 ** -7 if dk_dtype == torch.bfloat16 else 0.0)
+    assert ((dk.float() - dk1.float()).abs() <= tol).all()
+
+
+@pytest.mark.gpu
+def test_bwd_long_sequence_is_chunked(gpu):
+    # S = 8192 (B = 1, H = 16): the causal dS' blocks alone are ~1.1 GB, more than the 512 MiB
+    # cap, so the rows run in three chunks; references in fp32 on the GPU.
+    from python import _lib
+    ws = _lib.lib().dmla_bwd_workspace_bytes(1, 16, 8192, 8192, 576, 512, 1)
+    assert ws < (512 << 20) + (200 << 20), ws
+    q, k, do = _inputs(1, 16, 8192, 8192, seed=5)
+    _check(gpu, q, k, do, True, ref_device="gpu", autograd=False)
