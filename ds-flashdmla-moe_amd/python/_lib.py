@@ -11,7 +11,8 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_ROOT = os.path.dirname(_HERE)
-LIB_PATH = os.path.join(PKG_ROOT, "libflashdmla.so")
+# DMLA_LIBRARY names another build of the same ABI (the sanitizer build of csrc/Makefile).
+LIB_PATH = os.environ.get("DMLA_LIBRARY") or os.path.join(PKG_ROOT, "libflashdmla.so")
 
 DMLA_OK = 0
 DMLA_ERR_INVALID_ARG = -1
