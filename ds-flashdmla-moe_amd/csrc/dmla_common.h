@@ -58,6 +58,15 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
 
+// The lane index, recomputed where it is called: the compiler can neither hoist it out of an
+// enclosing loop nor share it with another call.  Per-lane offsets derived from it are then
+// computed where they are used instead of being kept live (and spilled) across a long loop.
+__device__ __forceinline__ int fresh_lane_id() {
+  int v;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(v));
+  return v;
+}
+
 // Wave-uniform value of an expression that is already uniform (moves it to an SGPR).
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 

@@ -162,7 +162,12 @@ __device__ __noinline__ void mqa_fwd_exact(const MqaParams* params, Work wk, DML
 // contains the (register-hungry) retry code.
 template <bool kDecode, int kHalf, bool kExact>
 __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams* params, const Work& wk,
-                                             DMLA_LDS char* lds, const int wave, const int lane) {
+                                             DMLA_LDS char* lds, const int wave, const int lane_arg) {
+  // Per-lane values are derived here, per work item, rather than once per kernel: kept live
+  // across every item's tile loop they would be spilled, and each reload's vmcnt wait would
+  // drain the copies and stores in flight.
+  (void)lane_arg;
+  const int lane = fresh_lane_id();
   const int l16 = lane & 15;
   const int g = lane >> 4;
   const int pair = wave >> 2;          // rows 32 pair .. +31 for the partial scores
