@@ -453,10 +453,7 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
   // ---- Q through LDS, with the first key tile in flight beside it ---------------------------
   // Chunk k of the staging area is 16-byte chunk k % 73 of row k / 73 (chunk 72 is the row's
   // padding and re-reads chunk 0); rows past the last one re-read row 0 of the item.
-  // (The first tile's copies go out before Q's: for decode, tile_src waits for the page-index
-  // loads, which would otherwise also drain the Q copies issued after them.)
-  if (tile_begin < tile_end) stage(tile_begin, tile_begin);
-  {
+  auto stage_q = [&]() {
     const unsigned qbase = lds_base + kQOffset;
     for (int i = wave; i * 64 < kQChunks; i += kWaves) {
       const int k = i * 64 + lane;
@@ -471,6 +468,33 @@ __device__ __forceinline__ void mqa_fwd_body(const MqaParams& p, const MqaParams
         qrow = p.q + b * p.q_sb + r * p.q_sh;
       }
       dma16_addr(qrow + 8 * (ch < kDqk / 8 ? ch : 0), qbase + i * 1024);
+    }
+  };
+  if constexpr (!kDecode) {
+    if (tile_begin < tile_end) stage(tile_begin, tile_begin);
+    stage_q();
+  } else {
+    // The Q copies go out first; the first tile's page index then comes through the scalar
+    // cache (lgkmcnt), so the Q copies and the page-index vector loads above stay in flight
+    // while it is fetched: the first tile's copies wait for one lookup instead of for the vector
+    // loads and everything issued with them.
+    stage_q();
+    int page0 = 0;
+    if (tile_begin < tile_end) {
+      const uint64_t ba = reinterpret_cast<uint64_t>(p.block_table + b * p.bt_sb + tile_begin / (kPage / kTileN));
+      const uint64_t bu = ((uint64_t)__builtin_amdgcn_readfirstlane((unsigned)(ba >> 32)) << 32) |
+                          (unsigned)__builtin_amdgcn_readfirstlane((unsigned)ba);
+      asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(page0) : "s"(bu) : "memory");
+      const bool bad = page0 < 0 || page0 >= p.num_pages;
+      bad_page = bad_page || bad;
+      const int pg = bad ? 0 : page0;
+      const char* src = reinterpret_cast<const char*>(p.kv + (int64_t)pg * p.k_sb +
+                                                      (int64_t)(tile_begin % (kPage / kTileN)) * kTileN * p.k_ss);
+      const unsigned dst = slot_addr(tile_begin);
+      const int valid_rows = wk.ctx - tile_begin * kTileN;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) copy_part(k, src, valid_rows, dst, Plain{}, Checked{});
+      if (ncopies > 4) copy_part(4, src, valid_rows, dst, Plain{}, Checked{});
     }
   }
   wait_vmem();
