@@ -144,7 +144,7 @@ constexpr int kInlinePlanB = kThreads;   // one sequence per thread
 constexpr int kInlinePlanR = kThreads;
 struct InlinePlan {
   int tp[kInlinePlanB + 1];    // tile prefix
-  int neb[kInlinePlanB + 1];   // nonempty sequences before b
+  int rfb[kInlinePlanR];       // first sequence of each range
   int ns[kInlinePlanB];        // split count
   int fr[kInlinePlanB];        // first range
   int sb[kInlinePlanB + 1];    // first partial slot
@@ -798,47 +798,35 @@ __device__ __forceinline__ void build_inline_plan(const MqaParams& p, DMLA_LDS I
   int total, nonempty;
   const int tpb = wg_exclusive_scan(nt, ip->tmp, total);
   const int nb = wg_exclusive_scan(nt > 0 ? 1 : 0, ip->tmp, nonempty);
-  if (tid < B) {
-    ip->tp[tid] = tpb;
-    ip->neb[tid] = nb;
-  }
-  if (tid == 0) ip->tp[B] = total;
   const int64_t weighted = (int64_t)total + (int64_t)kSegCost * nonempty;
   const int W = (int)max<int64_t>(1, (weighted + R - 1) / R);
-  __syncthreads();
-  // Range starts: weighted position r W -> the sequence holding it -> its tile (or the
-  // sequence's first tile when among its virtual ones).
-  for (int rr = tid; rr <= R; rr += kThreads) {
-    int t = total;
-    if (rr < R && (int64_t)rr * W < weighted) {
-      const int64_t pos = (int64_t)rr * W;
-      int lo = 0, hi = B - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) / 2;
-        if ((int64_t)ip->tp[mid] + (int64_t)kSegCost * ip->neb[mid] <= pos) lo = mid; else hi = mid - 1;
-      }
-      const int64_t off = pos - ((int64_t)ip->tp[lo] + (int64_t)kSegCost * ip->neb[lo]);
-      t = ip->tp[lo] + (int)max<int64_t>(0, off - kSegCost);
-      t = min(t, ip->tp[lo + 1]);
-    }
-    ip->rs[rr] = t;
-  }
-  __syncthreads();
-  auto range_of = [&](int t) {   // the last range starting at or before tile t
-    int lo = 0, hi = R - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) / 2;
-      if (ip->rs[mid] <= t) lo = mid; else hi = mid - 1;
-    }
-    return lo;
-  };
+  // Each nonempty sequence owns the weighted positions [ws, ws + kSegCost + nt): its kSegCost
+  // virtual tiles, then its tiles.  The ranges starting there (r W in that span) start at its
+  // first tile or at the tile under r W -- the value the plan kernel's search over sequences
+  // finds -- and a tile t of it lies in range floor((t + kSegCost (nb + 1)) / W), the last range
+  // starting at or before t.  So every thread places its sequence's ranges and splits itself,
+  // with no searches.
   int ns = 0, fr = 0;
   if (tid < B) {
-    const int tb = ip->tp[tid], te = ip->tp[tid + 1];
-    if (te > tb) {
-      fr = range_of(tb);
-      ns = range_of(te - 1) - fr + 1;
+    ip->tp[tid] = tpb;
+    if (nt > 0) {
+      const int64_t ws = (int64_t)tpb + (int64_t)kSegCost * nb;
+      const int64_t we = ws + kSegCost + nt;
+      const int r0 = (int)((ws + W - 1) / W), r1 = (int)min<int64_t>((we + W - 1) / W, R);
+      for (int r = r0; r < r1; ++r) {
+        ip->rs[r] = tpb + (int)max<int64_t>(0, (int64_t)r * W - ws - kSegCost);
+        ip->rfb[r] = tid;
+      }
+      const int64_t w1 = (int64_t)kSegCost * (nb + 1);
+      fr = (int)(((int64_t)tpb + w1) / W);
+      ns = (int)(((int64_t)tpb + nt - 1 + w1) / W) - fr + 1;
     }
+  }
+  if (tid == 0) ip->tp[B] = total;
+  // Ranges past the weighted total are empty.
+  for (int rr = (int)((weighted + W - 1) / W) + tid; rr <= R; rr += kThreads) {
+    ip->rs[rr] = total;
+    if (rr < R) ip->rfb[rr] = B - 1;
   }
   int nsplits;
   const int sbb = wg_exclusive_scan(ns, ip->tmp, nsplits);
@@ -866,15 +854,7 @@ __device__ __forceinline__ void build_inline_plan(const MqaParams& p, DMLA_LDS I
       first_range[i] = ip->fr[i];
     }
     for (int i = tid; i <= R; i += kThreads) range_start[i] = ip->rs[i];
-    for (int i = tid; i < R; i += kThreads) {
-      const int t = ip->rs[i];
-      int lo = 0, hi = B - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) / 2;
-        if (ip->tp[mid] <= t) lo = mid; else hi = mid - 1;
-      }
-      range_first_b[i] = lo;
-    }
+    for (int i = tid; i < R; i += kThreads) range_first_b[i] = ip->rfb[i];
     if (tid == 0) {
       plan[0] = B; plan[1] = R; plan[2] = W; plan[3] = total; plan[4] = nsplits; plan[5] = kSegCost;
       plan[6] = plan[7] = 0;
@@ -928,17 +908,7 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
     const int t0 = inl ? ip->rs[r] : range_start[r];
     const int t1 = inl ? ip->rs[r + 1] : range_start[r + 1];
     if (t0 >= t1) return;
-    int first_b;
-    if (inl) {
-      int lo = 0, hi = p.B - 1;   // the sequence holding tile t0
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) / 2;
-        if (ip->tp[mid] <= t0) lo = mid; else hi = mid - 1;
-      }
-      first_b = lo;
-    } else {
-      first_b = range_first_b[r];
-    }
+    const int first_b = inl ? ip->rfb[r] : range_first_b[r];
     const MqaParams* params = (const MqaParams*)(__builtin_amdgcn_kernarg_segment_ptr());
     for (int bseq = first_b; bseq < p.B; ++bseq) {
       const int tb = tp_of(bseq);
