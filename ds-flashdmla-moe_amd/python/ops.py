@@ -16,6 +16,7 @@ Conventions (the reference fixes none of them; see the oracle for the restated m
 from __future__ import annotations
 
 import ctypes
+import functools
 import math
 from typing import Optional, Tuple
 
@@ -58,10 +59,26 @@ def _check_fp16_range(name: str, t: torch.Tensor) -> None:
              f"{name} has entries outside fp16's finite range (|x| <= 65504)")
 
 
+def _on_tensor_device(fn):
+    """Runs an op with the device of its first GPU tensor argument current.  The library sizes
+    its work and workspace, finds its static scratch and launches on the current device, so
+    that must be the device the tensors live on (what a device guard does in a PyTorch
+    extension); with one GPU this changes nothing."""
+    @functools.wraps(fn)
+    def wrapped(*args, **kwargs):
+        for a in (*args, *kwargs.values()):
+            if isinstance(a, torch.Tensor) and a.is_cuda:
+                with torch.cuda.device(a.device):
+                    return fn(*args, **kwargs)
+        return fn(*args, **kwargs)
+    return wrapped
+
+
 def _scale(softmax_scale: Optional[float], d_qk: int) -> float:
     return float(softmax_scale) if softmax_scale is not None else 1.0 / math.sqrt(d_qk)
 
 
+@_on_tensor_device
 def flash_dmla_fwd(
     q: torch.Tensor,
     k_lat: torch.Tensor,
@@ -98,6 +115,7 @@ def flash_dmla_fwd(
     return o, m, l
 
 
+@_on_tensor_device
 def flash_dmla_fwd_onthefly(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -150,6 +168,7 @@ def flash_dmla_fwd_onthefly(
     return (o, m, l) if return_stats else o
 
 
+@_on_tensor_device
 def flash_dmla_decode_plan(cache_seqlens: torch.Tensor, num_heads: int, max_pages: int) -> torch.Tensor:
     """Decode tile-scheduler plan (int32 tensor) for this batch on the current device.
 
@@ -167,6 +186,7 @@ def flash_dmla_decode_plan(cache_seqlens: torch.Tensor, num_heads: int, max_page
     return plan
 
 
+@_on_tensor_device
 def flash_dmla_decode_paged(
     q: torch.Tensor,
     kv_pool: torch.Tensor,
@@ -242,6 +262,7 @@ def flash_dmla_decode_paged(
     return (o, lse) if return_lse else o
 
 
+@_on_tensor_device
 def flash_dmla_kv_append(
     kv_pool: torch.Tensor,
     block_table: torch.Tensor,
@@ -281,6 +302,7 @@ def flash_dmla_kv_append(
         _require(int(flag.item()) == 0, "kv append: a row's page slot or page index was out of range (row skipped)")
 
 
+@_on_tensor_device
 def flash_dmla_lse_combine(
     part_o: torch.Tensor,
     part_lse: torch.Tensor,
@@ -333,6 +355,7 @@ class FlashDMLACacheLatent(torch.autograd.Function):
         return dq, dk_lat.to(k_lat.dtype), None, None, None
 
 
+@_on_tensor_device
 def flash_dmla_bwd(
     q: torch.Tensor,
     k_lat: torch.Tensor,
@@ -392,6 +415,7 @@ def flash_dmla_bwd(
     return dq, dk
 
 
+@_on_tensor_device
 def flash_dmla_bwd_onthefly(
     q: torch.Tensor,
     k: torch.Tensor,
