@@ -9,6 +9,8 @@ B=4, H=16, S=2048, Q [B,H,S,576], shared K_lat [B,S,576], V_lat = K_lat[..., :51
 whole batch with inputs resident in HBM.  value = algorithmic TFLOP/s over the K timed steps,
 counting B*H*S(S+1)*(576+512) flops (unmasked causal pairs only).
 
+Before its W warmup launches, each workload runs untimed for clock_settle_s (0.1 s), so that
+the K timed launches see the settled shader clock rather than its ramp (see _settle).
 `roofline` times the kernel itself with HIP events recorded on the stream it is launched on;
 `traffic` comes from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary when present.
 `cpu_baseline` times the fp32 PyTorch eager oracle (oracle/dmla_ref.py) on the host cores
@@ -52,16 +54,41 @@ def _load_traffic(name):
         return json.load(f).get("hbm_bytes_per_launch")
 
 
+SETTLE_S = 0.1   # untimed load before each workload's warmup (seconds of wall time)
+
+
+def _settle(fn):
+    """Runs fn() untimed for SETTLE_S seconds (synchronizing every 8 launches); returns the
+    number of launches.  The shader clock ramps over the first tens of milliseconds of load:
+    the prefill kernel measured 323 us (median of 40) after 5 warmup launches, 285 us after 30
+    and 276-281 us once settled.  Every workload here also follows seconds of host-only work
+    (its input generation, the previous workload's CPU baseline) in which the clock drops
+    again.  Without this, a short --warmup would time the ramp instead of the kernel."""
+    import torch
+
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        for _ in range(8):
+            fn()
+        n += 8
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= SETTLE_S:
+            return n
+
+
 def _time_launches(fn, steps, warmup):
-    """Runs fn() warmup times, then `steps` timed times.  Returns (wall ms/step, kernel stats).
+    """Settles the clock (_settle), runs fn() warmup times, then `steps` timed times.  Returns
+    (wall ms/step, kernel stats).
 
     Wall time is bracketed by torch.cuda.synchronize() on both sides; per-launch durations
     come from HIP events recorded around each launch on the current stream, which is the
-    stream the C ABI receives and launches on.  The kernel figure is the median launch (the
-    first launches of a short run can still see the clock ramp); the mean is reported beside it.
+    stream the C ABI receives and launches on.  The kernel figure is the median launch; the
+    mean is reported beside it.
     """
     import torch
 
+    settle = _settle(fn)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -78,7 +105,7 @@ def _time_launches(fn, steps, warmup):
     mid = len(per) // 2
     median = per[mid] if len(per) % 2 else 0.5 * (per[mid - 1] + per[mid])
     return wall_ms, {"median": median, "mean": sum(per) / len(per), "min": per[0], "max": per[-1],
-                     "launches": len(per)}
+                     "launches": len(per), "settle_launches": settle}
 
 
 def _roofline(bound, work, stats, peak, unit, traffic, kernel, work_key):
@@ -87,7 +114,7 @@ def _roofline(bound, work, stats, peak, unit, traffic, kernel, work_key):
     return {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit, "frac": achieved / peak,
             "traffic": traffic, "kernel": kernel, "kernel_ms": stats["median"], "kernel_ms_mean": stats["mean"],
             "kernel_ms_min": stats["min"], "kernel_ms_max": stats["max"], "launches_timed": stats["launches"],
-            work_key: work}
+            "clock_settle_launches": stats["settle_launches"], work_key: work}
 
 
 def bench_prefill(steps, warmup, cpu_baseline):
@@ -475,6 +502,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1)*0.5 inputs of the benchmark config 2 shapes)",
         "config": primary["config"],
+        "clock_settle_s": SETTLE_S,
         "roofline": primary["roofline"],
         "cpu_baseline": primary.get("cpu_baseline"),
         "secondary": secondary,
