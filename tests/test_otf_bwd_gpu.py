@@ -12,7 +12,12 @@ rounding alone moves dwk by up to ~3e-2 at these sizes (the exact math fed with 
 bf16-rounded O, in fp64, against the exact gradient).  So against autograd each gradient may
 differ by that same-O error of the oracle plus 2e-2 max-abs, and by 1e-2 mean-rel.  dwk and dwv
 are compared in fp32, the op's default output type: they sum over every batch element and
-position and reach ~30 at config-4 sizes, where a bf16 rounding alone is 0.06.  Inputs follow benchmark config 4:
+position and reach ~30 at config-4 sizes, where a bf16 rounding alone is 0.06.  dq, dk and dv
+are bf16, and with few keys per row they reach 10-30 (2 keys, 233 rows: |dv| ~25), where one
+bf16 rounding of the exact value is already 0.03-0.1.  So each of their entries may also differ
+by that rounding of its reference (bf16's unit roundoff, 2^-8 relative).  test_otf_bwd_large_gradients
+covers gradients of 50-120, where the fp16 operands of the second-stage products alone exceed
+2e-2; it adds a normwise 2^-10 x max|ref| (two fp16 roundings) to the bar and says why.  Inputs follow benchmark config 4:
 q, k, v ~ N(0, 1), Xavier-uniform weights, scale 1/8, dO ~ N(0, 1).
 """
 import math
@@ -20,7 +25,7 @@ import math
 import pytest
 import torch
 
-from conftest import OUT_MAX_ABS, OUT_MEAN_REL, assert_out_close, seeded
+from conftest import BF16_ROUNDING, OUT_MAX_ABS, OUT_MEAN_REL, assert_out_close, assert_out_close_scaled, seeded
 from oracle import dmla_ref as R
 from python import ops
 
@@ -47,7 +52,7 @@ def _run(gpu, xs, causal, scale=0.125, **kw):
     return o, m, l, grads
 
 
-def _check(gpu, B, H, Sq, Sk, causal, seed, ref_device="cpu", autograd=True, scale=0.125):
+def _check(gpu, B, H, Sq, Sk, causal, seed, ref_device="cpu", autograd=True, scale=0.125, rel_max=0.0):
     xs = _inputs(B, H, Sq, Sk, seed)
     o, m, l, grads = _run(gpu, xs, causal, scale)
     assert [g.dtype for g in grads] == [torch.bfloat16] * 3 + [torch.float32] * 2
@@ -56,15 +61,18 @@ def _check(gpu, B, H, Sq, Sk, causal, seed, ref_device="cpu", autograd=True, sca
     ref = R.dmla_bwd_onthefly(q, k, v, wk, wv, o.to(dev).float(), do, m.to(dev), l.to(dev), scale, causal)
     for name, g, r in zip(NAMES, grads, ref):
         assert tuple(g.shape) == tuple(r.shape), name
-        assert_out_close(g, r, f"{name} vs oracle backward")
+        assert_out_close_scaled(g, r, f"{name} vs oracle backward", rel_max)
     if autograd:
         ag = R.dmla_grads_onthefly_autograd(q, k, v, wk, wv, do, scale, causal, torch.float32)
         for name, g, r, a in zip(NAMES, grads, ref, ag):
             a = a.to(g.device)
             same_o = (r.to(g.device) - a).abs().max().item()   # the bf16 O's share, no kernel involved
             diff = (g.float() - a).abs()
-            assert diff.max().item() <= same_o + OUT_MAX_ABS, \
-                f"{name} vs fp32 autograd: max-abs {diff.max().item():.3e} > {same_o:.3e} + {OUT_MAX_ABS}"
+            # bf16 outputs also carry their own rounding (2^-8 relative), as in the oracle check
+            allow = (same_o + OUT_MAX_ABS + rel_max * a.abs().max()
+                     + (a.abs() * BF16_ROUNDING if g.dtype == torch.bfloat16 else 0.0))
+            assert (diff <= allow).all(), \
+                f"{name} vs fp32 autograd: max-abs {diff.max().item():.3e} > {same_o:.3e} + {OUT_MAX_ABS} (+ bf16 rounding)"
             mean_rel = (diff.mean() / a.abs().mean().clamp_min(1e-30)).item()
             assert mean_rel <= OUT_MEAN_REL, f"{name} vs fp32 autograd: mean-rel {mean_rel:.3e}"
     return grads
@@ -88,6 +96,22 @@ def test_otf_bwd_small_shapes(gpu, B, H, Sq, Sk, causal):
     grads = _check(gpu, B, H, Sq, Sk, causal, seed=B * 100 + H * 10 + Sq)
     if causal and Sq > Sk:
         assert torch.equal(grads[0][:, :, :Sq - Sk].float().cpu(), torch.zeros(B, H, Sq - Sk, 64))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", [353, 5009])
+def test_otf_bwd_large_gradients(gpu, seed):
+    """Two keys seen by all 233 rows of two heads: the gradients sum hundreds of terms without
+    averaging out, |dk| ~12, |dv| ~25, |dwk| ~50, |dwv| ~120.  The second-stage products take fp16
+    operands (P, dS, and dK_lat / dV_lat stored for the weight gradients), and P is recomputed
+    from an fp16 K_lat.  Each of these roundings (2^-11 relative) carries an error proportional to
+    the size of the terms summed, not to the sum: with two keys, dwk[i, j] = k[0, i] dK_lat[0, j]
+    + k[1, i] dK_lat[1, j], whose terms often cancel.  In an fp64 emulation of the kernels'
+    roundings they reach ~0.017 on dwk and ~0.03 on dwv; the GPU's dwk differs by 2.35e-2 at an
+    entry whose reference is near 0 (4.4e-4 of max|dwk|).  No flat 2e-2 holds at these
+    magnitudes for fp16 operands, so the bar adds a normwise 2^-10 x max|ref| (two fp16
+    roundings) to every entry.  Every other case in this file is held to the flat bar."""
+    _check(gpu, 1, 2, 233, 2, False, seed=seed, rel_max=2.0 ** -10)
 
 
 @pytest.mark.gpu
