@@ -1,4 +1,5 @@
 // Error state and small host utilities behind the C ABI.
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 
@@ -27,15 +28,16 @@ int check_launch(const char* what) {
 }
 
 int device_cu_count() {
-  static int cache[64] = {0};
+  // Per device, filled on first use; threads that race there store the same value.
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 }  // namespace dmla
