@@ -50,6 +50,13 @@ def _check_bf16(name: str, t: torch.Tensor, ndim: int) -> None:
     _require(t.stride(-1) == 1, f"{name} must be contiguous in its last dim")
 
 
+def _same_device(**tensors: Optional[torch.Tensor]) -> None:
+    """Raises unless every given tensor lives on one device (the kernels read them all there)."""
+    devs = {name: t.device for name, t in tensors.items() if t is not None}
+    _require(len(set(devs.values())) <= 1, "tensors must be on one device, got " +
+             ", ".join(f"{n} on {d}" for n, d in devs.items()))
+
+
 def _check_fp16_range(name: str, t: torch.Tensor) -> None:
     """Raises unless every entry of t is finite and inside fp16's range (|x| <= 65504): the
     kernels convert these operands to fp16, which saturates beyond it.  One device sync."""
@@ -96,7 +103,7 @@ def flash_dmla_fwd(
     B, H, Sq, Dqk = q.shape
     _require(k_lat.shape[0] == B and k_lat.shape[2] == Dqk,
              f"k_lat shape {tuple(k_lat.shape)} does not match q {tuple(q.shape)}")
-    _require(q.device == k_lat.device, "q and k_lat must be on the same device")
+    _same_device(q=q, k_lat=k_lat)
     Sk = k_lat.shape[1]
     o = torch.empty((B, H, Sq, d_v), dtype=torch.bfloat16, device=q.device)
     m = l = None
@@ -148,6 +155,7 @@ def flash_dmla_fwd_onthefly(
     _require(tuple(wk.shape) == (H, Din, Dl) and tuple(wv.shape) == (H, Din, Dl),
              "wk and wv must be [H, d_in, d_lat]")
     _require(wk.stride() == wv.stride(), "wk and wv must share strides")
+    _same_device(q=q, k=k, v=v, wk=wk, wv=wv)
     if check_range:
         for name, t in (("q", q), ("k", k), ("v", v), ("wk", wk), ("wv", wv)):
             _check_fp16_range(name, t)
@@ -220,6 +228,7 @@ def flash_dmla_decode_paged(
     _require(Dk == Dqk, f"kv_pool last dim {Dk} != q last dim {Dqk}")
     _require(page == PAGE_SIZE, f"page size must be {PAGE_SIZE}, got {page}")
     _require(block_table.shape[0] == B and cache_seqlens.shape[0] == B, "batch size mismatch")
+    _same_device(q=q, kv_pool=kv_pool, block_table=block_table, cache_seqlens=cache_seqlens, plan=plan)
     max_pages = block_table.shape[1]
     if check_indices:
         bt = block_table.cpu()
@@ -287,6 +296,8 @@ def flash_dmla_kv_append(
     num_pages, P, dk = kv_pool.shape
     _require(dk == d, "kv_pool and new_kv row widths differ")
     _require(block_table.shape[0] == B and cache_seqlens.shape[0] == B, "batch size mismatch")
+    _same_device(kv_pool=kv_pool, block_table=block_table, cache_seqlens=cache_seqlens, new_kv=new_kv,
+                 new_lens=new_lens)
     if new_lens is not None:
         _require(new_lens.dtype == torch.int32 and new_lens.dim() == 1 and new_lens.is_cuda and new_lens.is_contiguous()
                  and new_lens.shape[0] == B, "new_lens must be a contiguous [B] int32 GPU tensor")
@@ -320,6 +331,7 @@ def flash_dmla_lse_combine(
     if num_splits is not None:
         _require(num_splits.dtype == torch.int32 and num_splits.is_cuda and num_splits.is_contiguous()
                  and tuple(num_splits.shape) == (B,), "num_splits must be a contiguous [B] int32 GPU tensor")
+    _same_device(part_o=part_o, part_lse=part_lse, num_splits=num_splits)
     o = torch.empty((B, H, d), dtype=torch.bfloat16, device=part_o.device)
     lse = torch.empty((B, H), dtype=torch.float32, device=part_o.device) if return_lse else None
     _lib.call(
@@ -392,6 +404,7 @@ def flash_dmla_bwd(
     for name, t in (("m", m), ("l", l)):
         _require(t.dtype == torch.float32 and t.is_cuda and t.is_contiguous() and tuple(t.shape) == (B, H, Sq),
                  f"{name} must be a contiguous float32 GPU tensor [B, H, Sq]")
+    _same_device(q=q, k_lat=k_lat, o=o, do=do, m=m, l=l)
     if check_range:
         for name, t in (("q", q), ("k_lat", k_lat), ("do", do)):
             _check_fp16_range(name, t)
@@ -458,6 +471,7 @@ def flash_dmla_bwd_onthefly(
     for name, t in (("m", m), ("l", l)):
         _require(t.dtype == torch.float32 and t.is_cuda and t.is_contiguous() and tuple(t.shape) == (B, H, Sq),
                  f"{name} must be a contiguous float32 GPU tensor [B, H, Sq]")
+    _same_device(q=q, k=k, v=v, wk=wk, wv=wv, o=o, do=do, m=m, l=l)
     if check_range:
         for name, t in (("q", q), ("k", k), ("v", v), ("do", do), ("wk", wk), ("wv", wv)):
             _check_fp16_range(name, t)

@@ -230,6 +230,15 @@ def test_fp16_range_check_rejects_values_the_kernels_would_saturate():
             ops._check_fp16_range("q", torch.tensor(bad).to(torch.bfloat16))
 
 
+def test_same_device_check_names_the_tensors_on_other_devices():
+    # Every op checks that its tensors share one device before any launch (absent optional
+    # tensors are skipped).
+    a, b = torch.zeros(2), torch.zeros(2, device="meta")
+    ops._same_device(q=a, k=torch.ones(3), plan=None)
+    with pytest.raises(ValueError, match="k on meta"):
+        ops._same_device(q=a, k=b)
+
+
 def test_onthefly_forward_wrapper_takes_check_range():
     import inspect
     assert "check_range" in inspect.signature(ops.flash_dmla_fwd_onthefly).parameters
