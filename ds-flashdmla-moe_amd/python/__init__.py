@@ -17,3 +17,4 @@ from .ops import (  # noqa: F401
     flash_dmla_onthefly,
 )
 from ._lib import DmlaError, DmlaInvalidArgument, DmlaUnsupported  # noqa: F401
+from . import torch_ops  # noqa: F401,E402  (registers torch.ops.flashdmla.*)
