@@ -32,8 +32,8 @@ __device__ __forceinline__ f32x4 load_part4(const T* p) {
 }
 
 template <typename T>
-__device__ __forceinline__ void combine_pair(const CombineArgs& a, const T* part, int b, int h, int n, int lane) {
-  const int64_t s0 = a.split_base != nullptr ? (int64_t)a.split_base[b] : 0;
+__device__ __forceinline__ void combine_pair(const CombineArgs& a, const T* part, int b, int h, int n, int64_t s0,
+                                             int lane) {
   const int64_t lbase = (a.split_base != nullptr ? s0 * a.lse_ss : (int64_t)b * a.lse_sb) + (int64_t)h * a.lse_sh;
   const int64_t obase = (a.split_base != nullptr ? s0 * a.po_ss : (int64_t)b * a.po_sb) + (int64_t)h * a.po_sh;
   bf16* orow = a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
@@ -105,27 +105,45 @@ __device__ __forceinline__ void combine_pair(const CombineArgs& a, const T* part
   if (lane == 0 && a.lse != nullptr) a.lse[(int64_t)b * a.H + h] = wsum > 0.f ? mref + __logf(wsum) : mx;
 }
 
+// kPlan: the decode case, split_base and num_splits both given, so that both loads go out
+// together (one round trip before the partials' loads, not one per null check).
+template <bool kPlan>
 __global__ void __launch_bounds__(256) lse_combine_kernel(CombineArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t pair = (int64_t)blockIdx.x * 4 + uniform(threadIdx.x >> 6);
-  if (pair >= (int64_t)a.B * a.H) return;
-  const int b = (int)(pair / a.H), h = (int)(pair - (int64_t)b * a.H);
+  // 32-bit index math: the launcher checks B * H < 2^31
+  const unsigned pair = blockIdx.x * 4u + (unsigned)uniform(threadIdx.x >> 6);
+  if (pair >= (unsigned)(a.B * a.H)) return;
+  const int b = (int)(pair / (unsigned)a.H), h = (int)(pair - (unsigned)b * (unsigned)a.H);
   int n = a.max_splits;
-  if (a.num_splits != nullptr) {
-    n = min(max(a.num_splits[b], 0), a.max_splits);
-  } else if (a.seqlens != nullptr) {
-    const int ctx = min(max(a.seqlens[b], 0), a.max_pages * a.page_size);
-    const int npages = (ctx + a.page_size - 1) / a.page_size;
-    n = max(1, (npages + a.pages_per_split - 1) / a.pages_per_split);
+  int64_t s0 = 0;
+  if constexpr (kPlan) {
+    int sb = a.split_base[b], ns = a.num_splits[b];
+    asm volatile("" : "+s"(sb), "+s"(ns));   // both loads issued before anything waits on either
+    s0 = sb;
+    n = min(max(ns, 0), a.max_splits);
+  } else {
+    if (a.split_base != nullptr) s0 = a.split_base[b];
+    if (a.num_splits != nullptr) {
+      n = min(max(a.num_splits[b], 0), a.max_splits);
+    } else if (a.seqlens != nullptr) {
+      const int ctx = min(max(a.seqlens[b], 0), a.max_pages * a.page_size);
+      const int npages = (ctx + a.page_size - 1) / a.page_size;
+      n = max(1, (npages + a.pages_per_split - 1) / a.pages_per_split);
+    }
   }
   if (a.skip_single && n == 1) return;   // the decode kernel already wrote such rows itself
-  if (a.part_o16 != nullptr) combine_pair(a, a.part_o16, b, h, n, lane);
-  else combine_pair(a, a.part_o, b, h, n, lane);
+  if (a.part_o16 != nullptr) combine_pair(a, a.part_o16, b, h, n, s0, lane);
+  else combine_pair(a, a.part_o, b, h, n, s0, lane);
 }
 
 int launch_lse_combine(const CombineArgs& a, hipStream_t stream, const char* what) {
   if (a.B == 0 || a.H == 0) return DMLA_OK;
-  hipLaunchKernelGGL(lse_combine_kernel, dim3((unsigned)(((int64_t)a.B * a.H + 3) / 4)), dim3(256), 0, stream, a);
+  if ((int64_t)a.B * a.H >= ((int64_t)1 << 31)) return fail(DMLA_ERR_UNSUPPORTED, "%s: B * H must be below 2^31", what);
+  const dim3 grid((unsigned)(((int64_t)a.B * a.H + 3) / 4));
+  if (a.split_base != nullptr && a.num_splits != nullptr)
+    hipLaunchKernelGGL(lse_combine_kernel<true>, grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(lse_combine_kernel<false>, grid, dim3(256), 0, stream, a);
   return check_launch(what);
 }
 
