@@ -75,3 +75,32 @@ def test_prefill_forward_and_backward_replay_in_a_graph(gpu):
         torch.cuda.synchronize()
         for name, g, e in zip(("o", "dq", "dk_lat"), outs_g, outs_e):
             assert torch.equal(g, e), f"replay {r}: {name} differs from the eager call"
+
+
+@pytest.mark.gpu
+def test_ops_launch_on_the_current_stream(gpu):
+    # Ops take the caller's current stream: an append and the decode that reads its rows,
+    # issued back to back on a side stream with no host synchronization in between, are
+    # ordered by that stream; results equal the same calls on the default stream.  The rows
+    # appended (inside each sequence's last page) held NaN before, so a decode that ran ahead
+    # of the append would not be finite.
+    q0, pool0, table0, lens0 = _paged([300, 60, 1000], 32, seed=92)
+    q, table, lens = q0.to(gpu), table0.to(gpu), lens0.to(gpu)
+    new = seeded((3, 4, 576), 93, 0.5, torch.bfloat16).to(gpu)
+    grown = lens + 4
+
+    def run():
+        pool = pool0.to(gpu)
+        ops.flash_dmla_kv_append(pool, table, lens, new)
+        return ops.flash_dmla_decode_paged(q, pool, table, grown, 512, SCALE, return_lse=True)
+
+    o_ref, lse_ref = run()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        o_s, lse_s = run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(o_s).all()) and bool(torch.isfinite(lse_s).all())
+    assert torch.equal(o_s, o_ref) and torch.equal(lse_s, lse_ref)
