@@ -215,7 +215,7 @@ int dmla_kv_append(void* kv_pool, const int32_t* block_table, const int32_t* cac
  *
  *   o = sum_s w_s o_s / sum_s w_s with w_s = exp(lse_s - max_s lse_s), lse = max + log(sum w);
  *   a sequence whose splits all have lse = -inf gets o = 0 and lse = -inf; a NaN lse in any
- *   split makes o and lse NaN.  d % 4 == 0.
+ *   split makes o and lse NaN.  d % 4 == 0 and B * H < 2^31.
  */
 int dmla_lse_combine(const float* part_o, const float* part_lse, const int32_t* num_splits, void* o,
                      float* lse, int64_t B, int64_t H, int64_t max_splits, int64_t d, int64_t po_sb,
