@@ -171,6 +171,7 @@ def test_kv_append_and_combine_argument_errors():
     assert combine(po=None) == _lib.DMLA_ERR_INVALID_ARG
     assert combine(S=0) == _lib.DMLA_ERR_INVALID_ARG
     assert combine(d=6) == _lib.DMLA_ERR_UNSUPPORTED
+    assert combine(B=1 << 16, H=1 << 15) == _lib.DMLA_ERR_UNSUPPORTED   # B * H = 2^31, before any launch
     assert combine(B=0) == _lib.DMLA_OK
 
 
