@@ -120,3 +120,43 @@ def test_opcheck_accepts_the_registrations(gpu):
     torch.library.opcheck(F.decode_paged.default, (qp, pool, table, lens, 512, SCALE, None), test_utils=checks)
     new = seeded((2, 3, 576), 91, 0.5, torch.bfloat16).to(gpu)
     torch.library.opcheck(F.kv_append.default, (pool.clone(), table, lens, new, None), test_utils=checks)
+
+
+@pytest.mark.gpu
+def test_torch_compile_traces_the_ops(gpu):
+    # Dynamo + AOTAutograd over the registered ops (fake implementations for tracing, the
+    # autograd formula for the backward graph, auto-functionalization of the in-place append),
+    # run eagerly from the traced graphs: results equal the uncompiled calls bit for bit.
+    torch._dynamo.reset()
+    q, k, do = (t.to(gpu) for t in cl_inputs(1, 3, 70, 90, seed=92))
+
+    def train_step(q, k, do):
+        o = F.fwd_cache_latent(q, k, 512, SCALE, True)[0]
+        (o.float() * do.float()).sum().backward()
+        return o
+
+    compiled = torch.compile(train_step, backend="aot_eager", fullgraph=False)
+    qa, ka = q.clone().requires_grad_(), k.clone().requires_grad_()
+    oa = compiled(qa, ka, do)
+    qb, kb = q.clone().requires_grad_(), k.clone().requires_grad_()
+    ob = train_step(qb, kb, do)
+    _same(oa.detach(), ob.detach(), "o under torch.compile")
+    _same(qa.grad, qb.grad, "dq under torch.compile")
+    _same(ka.grad, kb.grad, "dk_lat under torch.compile")
+
+    qp, pool, table, lens = (t.to(gpu) for t in _paged([300, 60, 1000], 16, seed=93))
+    new = seeded((3, 1, 576), 94, 0.5, torch.bfloat16).to(gpu)
+
+    def decode_step(qp, pool, table, lens, new):
+        F.kv_append(pool, table, lens, new, None)
+        grown = lens + 1
+        plan = F.decode_plan(grown, 16, table.shape[1])
+        return F.decode_paged(qp, pool, table, grown, 512, SCALE, plan)
+
+    step = torch.compile(decode_step, backend="aot_eager", fullgraph=True)
+    pa, pb = pool.clone(), pool.clone()
+    oa, lsea = step(qp, pa, table, lens, new)
+    ob, lseb = decode_step(qp, pb, table, lens, new)
+    _same(pa, pb, "pool after the traced append")
+    _same(oa, ob, "decode o under torch.compile")
+    _same(lsea, lseb, "decode lse under torch.compile")
