@@ -11,9 +11,10 @@ counting B*H*S(S+1)*(576+512) flops (unmasked causal pairs only).
 
 Before its W warmup launches, each workload runs untimed for clock_settle_s (0.1 s), so that
 the K timed launches see the settled shader clock rather than its ramp (see _settle).
-The K timed steps carry one HIP event pair around all of them (no per-launch events, which
-add GPU time between launches); `roofline` times the kernel itself with HIP events recorded
-around each of K further launches on the stream it is launched on;
+The K timed steps carry one HIP event pair around all of them on the launch stream (no
+per-launch events, which add GPU time between launches); `roofline.achieved` divides the
+algorithmic work by that GPU time per step, and K further launches with HIP events around each
+give the per-launch median, mean and spread beside it;
 `traffic` comes from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary when present.
 `cpu_baseline` times the fp32 PyTorch eager oracle (oracle/dmla_ref.py) on the host cores
 (at most 16 threads) over the same workload, repeated for about --cpu-seconds seconds.
@@ -122,8 +123,9 @@ def _time_launches(fn, steps, warmup):
 
 
 def _roofline(bound, work, stats, peak, unit, traffic, kernel, work_key):
-    """roofline object from the median launch; the mean and spread ride along."""
-    achieved = work / (stats["median"] * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+    """roofline object: achieved from the timed steps' GPU time per step (one event pair around
+    all K of them); the per-launch median, mean and spread of the evented pass ride along."""
+    achieved = work / (stats["region_ms"] * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
     return {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit, "frac": achieved / peak,
             "traffic": traffic, "kernel": kernel, "kernel_ms": stats["median"], "kernel_ms_mean": stats["mean"],
             "kernel_ms_min": stats["min"], "kernel_ms_max": stats["max"], "launches_timed": stats["launches"],
