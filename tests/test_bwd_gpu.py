@@ -16,7 +16,7 @@ import math
 import pytest
 import torch
 
-from conftest import assert_out_close, seeded
+from conftest import OUT_MAX_ABS, assert_out_close, seeded
 from oracle import dmla_ref as R
 from python import ops
 
@@ -45,11 +45,26 @@ def _check(gpu, q, k, do, causal, scale=SCALE, ref_device="cpu", autograd=True):
     qf, kf, dof = q.to(dev).float(), k.to(dev).float(), do.to(dev).float()
     dq_ref, dk_ref = R.dmla_bwd_cache_latent(qf, kf, o.to(dev).float(), dof, m.to(dev), l.to(dev), 512, scale,
                                              causal)
-    assert_out_close(dq, dq_ref, "dq vs oracle backward")
+    # One key: every row that sees it has softmax 1 and the exact dS = dP - D is 0, so the exact
+    # dq is 0.  What remains is rounding: D comes from the saved bf16 O, dP from V itself, in the
+    # oracle as in the kernel.  Only the absolute bar applies to dq then (mean-rel against a
+    # reference that is itself rounding noise means nothing), against fp32 autograd (exactly 0)
+    # with the bf16 O's share (oracle - autograd) allowed, as test_bwd_single_key states.
+    single_key = k.shape[1] == 1
+    if single_key:
+        err = (dq.float() - dq_ref.to(dq.device)).abs().max().item()
+        assert err <= OUT_MAX_ABS, f"dq of a single key vs oracle backward: max-abs {err:.3e}"
+    else:
+        assert_out_close(dq, dq_ref, "dq vs oracle backward")
     assert_out_close(dk, dk_ref, "dk_lat vs oracle backward")
     if autograd:
         dq_ag, dk_ag = R.dmla_grads_autograd(qf, kf, dof, 512, scale, causal, torch.float32)
-        assert_out_close(dq, dq_ag, "dq vs fp32 autograd")
+        if single_key:
+            same_o = (dq_ref - dq_ag).abs().max().item()
+            err = (dq.float() - dq_ag.to(dq.device)).abs().max().item()
+            assert err <= same_o + OUT_MAX_ABS, f"dq of a single key vs fp32 autograd: max-abs {err:.3e}"
+        else:
+            assert_out_close(dq, dq_ag, "dq vs fp32 autograd")
         assert_out_close(dk, dk_ag, "dk_lat vs fp32 autograd")
     return dq, dk
 
