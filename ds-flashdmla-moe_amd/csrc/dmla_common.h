@@ -118,11 +118,17 @@ __device__ __forceinline__ void dma16_after_v(const void* sbase, unsigned voff, 
                : "s"(sl), "v"(voff), "s"(reinterpret_cast<const void*>(sb)), "v"(d0), "v"(d1), "v"(d2), "v"(d3)
                : "m0");
 }
-// A 4-byte global -> LDS load per lane (lane l writes lds_addr + 4 l): used to pull lines into
-// L2 ahead of their real copies; the LDS bytes written are a scratch area nobody reads.
-__device__ __forceinline__ void dma4_addr(const void* gaddr, unsigned lds_addr) {
+// 4-byte direct global->LDS copy of one wave: lane l reads sbase + voff and lands at
+// lds_addr + 4*l (per-row scalars staged beside a tile).
+__device__ __forceinline__ void dma4(const void* sbase, unsigned voff, unsigned lds_addr) {
+  const uint64_t base = reinterpret_cast<uint64_t>(sbase);
+  const uint64_t sb = ((uint64_t)__builtin_amdgcn_readfirstlane((unsigned)(base >> 32)) << 32) |
+                      (unsigned)__builtin_amdgcn_readfirstlane((unsigned)base);
   const unsigned sl = __builtin_amdgcn_readfirstlane(lds_addr);
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" : : "s"(sl), "v"(gaddr) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2"
+               :
+               : "s"(sl), "v"(voff), "s"(reinterpret_cast<const void*>(sb))
+               : "memory", "m0");
 }
 // Same copy with a full 64-bit global address per lane (rows of one tile that are far apart,
 // e.g. query rows of different heads).

@@ -3,32 +3,40 @@
 //     K_lat = K[b,:,h,:] WK[h],  V_lat = V[b,:,h,:] WV[h]        (README.md:14)
 // with respect to Q, K, V, WK and WV, from the forward's saved row statistics m and l
 // (README.md:12).  The attention part is the intended FA2 backward of
-// csrc/attention/fa2_bwd.cu:198-310 (D = rowsum(dO * O), dS = P * (dP - D), dV_lat = P^T dO,
-// dK_lat = scale dS^T Q, dQ = scale dS K_lat) with the softmax scale applied to dQ and dK_lat;
+// csrc/attention/fa2_bwd.cu:198-310 (D = rowsum(dO * O), dS = P * (dP - D), dV = P^T dO,
+// dK = scale dS^T Q, dQ = scale dS K) with the softmax scale applied to dQ and dK_lat;
 // the projections then give
 //     dK = dK_lat WK^T,  dWK[h] = sum_{b,s} K[b,s,h,:]^T dK_lat[b,h,s,:]   (same for V / WV).
 // The reference has no on-the-fly backward at all (WK / WV are learnable per README.md:14).
 //
 // Seven kernels run in order on one stream, all deterministic (no atomics):
-//   otf_bwd_prep_kernel    per query row: Q and dO as fp16, lse2 = (m + ln l) log2(e), D;
+//   otf_bwd_prep_kernel    per query row: lse2 = (m + ln l) log2(e) and -D;
 //   otf_bwd_wt_kernel      WK^T and WV^T;
-//   otf_bwd_proj_kernel    K_lat and V_lat as fp16 (the forward's projection products);
+//   otf_bwd_proj_kernel    K_lat and V_lat as fp16, for the dQ kernel;
 //   otf_bwd_dkdv_kernel    per 128 keys: dK_lat, dV_lat over the rows that see them;
 //   otf_bwd_dq_kernel      per 128 rows: dQ over the keys they see (S and dP recomputed);
 //   otf_bwd_wgrad_kernel   per (tensor, head, 1024 keys): dK / dV and a dWK / dWV partial;
 //   otf_bwd_wreduce_kernel sums the partials of each head in a fixed order.
 //
-// Every product runs on v_mfma_f32_16x16x32_f16 with fp32 accumulation: Q, dO, K, V and the
-// weights are converted to fp16 exactly (bf16's significand fits fp16's; |x| <= 65504), and the
-// rounded intermediates (K_lat, V_lat, P, dS, dK_lat, dV_lat) are fp16.  V_lat equals the
-// forward's (same operands, same order, same rounding); K_lat is the forward's fp32 projection
-// rounded once to fp16, where the forward keeps a bf16 hi + lo pair for its scores, so the
-// recomputed P carries the fp16 rounding of the scores (~2^-12 relative) against the forward's
-// exact statistics -- well inside the gradients' tolerance.  The one layout trick used
-// throughout: an MFMA C tile (lane l holds rows 4(l/16)+i, column l%16) of two 16-row blocks is
-// the B operand of a product contracting over those 32 rows when the k-index runs over rows
-// {4g+i} then {16+4g+i} (g = l/16); ds_read_b64_tr_b16 on a row-major tile hands the A operand
-// exactly that row order (two reads, rows 4g.. and 16+4g..).  So P and dS never go through LDS.
+// Precision.  dK_lat and dV_lat sum one term per row that sees a key, and through them dk, dv
+// and the weight gradients grow with the rows per key (non-causal attention over a few keys,
+// large batches): |dwv| passes 100 with two keys under 233 rows.  An operand rounded once to
+// 16 bits (2^-11 relative for fp16) then moves them by more than 2e-2.  So the dK / dV side
+// carries every rounded operand as a bf16 pair hi + lo (hi + lo within 2^-16 relative):
+//   * K_lat (times scale log2 e) and V_lat, projected in the dK/dV kernel itself from the raw
+//     rows, for the recomputed S (so P matches the forward's statistics, which the forward
+//     also scores with a bf16 hi + lo K_lat) and dP;
+//   * P and dS, the operands of dV_lat^T += dO^T P and dK_lat^T += Q^T dS;
+//   * dK_lat and dV_lat, stored as two bf16 planes for the weight-gradient kernel.
+// Q, dO, K, V and the weights are bf16 already, so they enter the bf16 MFMAs exactly and each
+// hi + lo operand costs one more MFMA.  dQ sums over the keys of one row and does not grow
+// that way: its kernel keeps fp16 operands (Q, dO, K_lat, V_lat, dS rounded to fp16, ~2^-11).
+//
+// The one layout trick used throughout: an MFMA C tile (lane l holds rows 4(l/16)+i, column
+// l%16) of two 16-row blocks is the B operand of a product contracting over those 32 rows when
+// the k-index runs over rows {4g+i} then {16+4g+i} (g = l/16); ds_read_b64_tr_b16 on a
+// row-major tile hands the A operand exactly that row order (two reads, rows 4g.. and 16+4g..).
+// So P and dS never go through LDS.
 #include <type_traits>
 
 #include "dmla_common.h"
@@ -39,13 +47,14 @@ namespace {
 
 constexpr int kIn = 128;                // raw K / V dims per head
 constexpr int kLat = 64;                // latent dims (Q, K_lat, V_lat, O)
-constexpr int kRowBlk = 128;            // dQ workgroup rows; Q rows are padded to a multiple
+constexpr int kRowBlk = 128;            // dQ workgroup rows; row statistics are padded to a multiple
 constexpr int kKeyBlk = 128;            // dK/dV workgroup keys; keys are padded to a multiple
 constexpr int kChunk = 1024;            // keys per weight-gradient workgroup
-constexpr int kTile = 32 * kLat * 2;    // one 32-row fp16 tile of 64 columns (4 KB)
+constexpr int kTile = 32 * kLat * 2;    // one 32-row tile of 64 16-bit columns (4 KB)
 constexpr int kStage = 4 * kTile;       // 64 rows of two tensors (16 KB)
-constexpr int kXTile = 32 * kIn * 2;    // one 32-key fp16 tile of 128 raw columns (8 KB)
-constexpr int kWgStage = 2 * kXTile + 2 * kTile;   // 64 keys: raw X and dX_lat (24 KB)
+constexpr int kRowStage = kStage + 512; // dK/dV stage: 64 rows of Q and dO, then their lse2 and -D
+constexpr int kXTile = 32 * kIn * 2;    // one 32-key tile of 128 raw bf16 columns (8 KB)
+constexpr int kWgStage = 2 * kXTile + 4 * kTile;   // 64 keys: raw X, dX_lat hi, dX_lat lo (32 KB)
 
 struct OtfBwdParams {
   const bf16* q;
@@ -57,12 +66,12 @@ struct OtfBwdParams {
   const bf16* dout;
   const float* m;   // [B, H, Sq] contiguous
   const float* l;
-  bf16* dq;
-  bf16* dk;
-  bf16* dv;
+  void* dq;             // bf16, or fp32 when dq_fp32
+  void* dk;             // bf16, or fp32 when dkv_fp32
+  void* dv;
   void* dwk;            // bf16, or fp32 when dw_fp32
   void* dwv;
-  int dw_fp32;
+  int dq_fp32, dkv_fp32, dw_fp32;
   int64_t q_sb, q_sh, q_ss, k_sb, k_ss, k_sh, v_sb, v_ss, v_sh, w_sh, w_si;
   int64_t o_sb, o_sh, o_ss, do_sb, do_sh, do_ss;
   int64_t dq_sb, dq_sh, dq_ss, dk_sb, dk_ss, dk_sh, dw_sh, dw_si;
@@ -70,14 +79,11 @@ struct OtfBwdParams {
   int Sqp, Skp;          // rows / keys padded to multiples of 128
   int n_sc;              // 1024-key chunks per batch element (weight gradients)
   float scale, scale_log2;
-  _Float16* q16;         // [B*H][Sqp][64]; padding rows zero
-  _Float16* do16;        // [B*H][Sqp][64]
   float* lse2;           // [B*H][Sqp]: (m + ln l) log2(e); padding and empty rows +inf
   float* nd;             // [B*H][Sqp]: -D = -rowsum(dO * O); padding rows 0
-  _Float16* klat;        // [B*H][Skp][64]; padding keys zero
-  _Float16* vlat;
-  _Float16* dklat;       // [B*H][Skp][64]; padding keys zero
-  _Float16* dvlat;
+  _Float16* klat;        // [B*H][Skp][64] fp16 K_lat * scale log2(e); padding keys zero
+  _Float16* vlat;        // [B*H][Skp][64] fp16 V_lat
+  bf16* dxlat;           // [4][B*H][Skp][64]: dK_lat hi, dK_lat lo, dV_lat hi, dV_lat lo
   float* wpart;          // [2][H][B*n_sc][128][64] fp32 partial weight gradients
   bf16* wt;              // [2][H][64][128]: WK^T, WV^T
 };
@@ -86,27 +92,62 @@ __device__ __forceinline__ f16x8 to_f16(const bf16x8& x) {
   return bf16_to_f16(__builtin_shufflevector(x, x, 0, 1, 2, 3), __builtin_shufflevector(x, x, 4, 5, 6, 7));
 }
 __device__ __forceinline__ f16x8 lds_f16x8(const DMLA_LDS char* p) { return *reinterpret_cast<const DMLA_LDS f16x8*>(p); }
+__device__ __forceinline__ bf16x8 lds_bf16x8(const DMLA_LDS char* p) { return *reinterpret_cast<const DMLA_LDS bf16x8*>(p); }
 // A column operand (k along tile rows) of a 32-row tile: rows 4g..4g+3 then 16+4g..16+4g+3.
 __device__ __forceinline__ f16x8 lds_col_operand(const DMLA_LDS char* tile, int lane, int cb) {
   const f16x4 a = lds_read_tr16_f16(reinterpret_cast<const DMLA_LDS f16x4*>(tile + col_operand_off(lane, cb, 0)));
   const f16x4 b = lds_read_tr16_f16(reinterpret_cast<const DMLA_LDS f16x4*>(tile + col_operand_off(lane, cb, 1)));
   return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
+__device__ __forceinline__ bf16x8 lds_col_operand_bf(const DMLA_LDS char* tile, int lane, int cb) {
+  return concat(lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tile + col_operand_off(lane, cb, 0))),
+                lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(tile + col_operand_off(lane, cb, 1))));
+}
 
-// Copies 64 rows of two [rows][64] fp16 arrays (rows row0 .. row0+63 of each) into a stage:
-// [x0 rows 0-31, x0 rows 32-63, x1 rows 0-31, x1 rows 32-63], each a 32-row tile in the
-// tile_chunk_off layout.  Sixteen 1 KB wave copies, four per wave; lane l of copy `part` lands
-// at byte 16 l of that 1 KB, i.e. tile row 8 part + l/8, physical chunk l%8.
-__device__ __forceinline__ void stage_pair(const _Float16* x0, const _Float16* x1, int row0, unsigned lds_stage,
-                                           int wave, int lane) {
+// v as a bf16 pair: hi = v's upper 16 bits (truncation), lo = v - hi (exact in fp32) rounded to
+// bf16.  |v - hi| < 2^-7 |v| and lo's rounding is 2^-9 of that, so hi + lo is within 2^-16 |v|.
+// Three VALU instructions per value: an AND and a subtract per value, one byte permute per two
+// hi halves, one packed conversion per two lo values.
+__device__ __forceinline__ void split_bf16(const float (&v)[8], bf16x8& hi, bf16x8& lo) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 h;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const unsigned a = __float_as_uint(v[2 * e]), b = __float_as_uint(v[2 * e + 1]);
+    h[e] = __builtin_amdgcn_perm(b, a, 0x07060302u);   // [a's upper half, b's upper half]
+    lo[2 * e] = (bf16)(v[2 * e] - __uint_as_float(a & 0xffff0000u));
+    lo[2 * e + 1] = (bf16)(v[2 * e + 1] - __uint_as_float(b & 0xffff0000u));
+  }
+  hi = __builtin_bit_cast(bf16x8, h);
+}
+// The same with hi rounded to nearest (|v - hi| <= 2^-9 |v|, hi + lo within 2^-17 |v|); for
+// values computed once per kernel, where the extra instructions do not matter.
+template <int N>
+__device__ __forceinline__ void split_bf16_rn(const float (&v)[N], __bf16 (&hi)[N], __bf16 (&lo)[N]) {
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    hi[e] = (bf16)v[e];
+    lo[e] = (bf16)(v[e] - (float)hi[e]);
+  }
+}
+
+// Copies 64 rows of two [rows][64] 16-bit arrays into a stage: [x0 rows 0-31, x0 rows 32-63,
+// x1 rows 0-31, x1 rows 32-63], each a 32-row tile in the tile_chunk_off layout.  Rows
+// row0 .. row0+63 of x (row r at x0 + r * ss0); rows at or past `rows` re-read row rows-1.
+// Sixteen 1 KB wave copies, four per wave; lane l of copy `part` lands at byte 16 l of that
+// 1 KB, i.e. tile row 8 part + l/8, physical chunk l%8.  ss * 128 must stay below 2^32.
+__device__ __forceinline__ void stage_pair(const void* x0, int64_t ss0, const void* x1, int64_t ss1, int row0,
+                                           int rows, unsigned lds_stage, int wave, int lane) {
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int n = 4 * wave + c;                  // 0 .. 15
     const int x = n >> 3, t = (n >> 2) & 1, part = n & 3;
     const int row = 8 * part + (lane >> 3);
     const int lc = (lane & 7) ^ swz(row & 15);   // logical chunk stored at this physical slot
-    const unsigned voff = 2u * (unsigned)((row0 + 32 * t + row) * kLat + 8 * lc);
-    dma16(x ? x1 : x0, voff, lds_stage + (2 * x + t) * kTile + part * 1024);
+    const int64_t ss = x ? ss1 : ss0;
+    const int rel = min(row0 + 32 * t + row, rows - 1) - row0;
+    const char* base = static_cast<const char*>(x ? x1 : x0) + 2 * (int64_t)row0 * ss;
+    dma16(base, 2u * (unsigned)(rel * ss + 8 * lc), lds_stage + (2 * x + t) * kTile + part * 1024);
   }
 }
 
@@ -116,20 +157,13 @@ __global__ void __launch_bounds__(256) otf_bwd_prep_kernel(OtfBwdParams p) {
   const int bh = blockIdx.y;
   const int b = bh / p.H, h = bh % p.H;
   const int r = blockIdx.x * 32 + (threadIdx.x >> 3), c = threadIdx.x & 7;
-  f16x8 q16 = {}, d16 = {};
   float dsum = 0.f;
   if (r < p.Sq) {
-    const bf16x8 qv = *reinterpret_cast<const bf16x8*>(p.q + b * p.q_sb + h * p.q_sh + (int64_t)r * p.q_ss + 8 * c);
     const bf16x8 ov = *reinterpret_cast<const bf16x8*>(p.o + b * p.o_sb + h * p.o_sh + (int64_t)r * p.o_ss + 8 * c);
     const bf16x8 dv = *reinterpret_cast<const bf16x8*>(p.dout + b * p.do_sb + h * p.do_sh + (int64_t)r * p.do_ss + 8 * c);
 #pragma unroll
     for (int e = 0; e < 8; ++e) dsum += (float)dv[e] * (float)ov[e];
-    q16 = to_f16(qv);
-    d16 = to_f16(dv);
   }
-  const size_t out = ((size_t)bh * p.Sqp + r) * kLat + 8 * c;
-  *reinterpret_cast<f16x8*>(p.q16 + out) = q16;
-  *reinterpret_cast<f16x8*>(p.do16 + out) = d16;
   dsum += __shfl_xor(dsum, 1);
   dsum += __shfl_xor(dsum, 2);
   dsum += __shfl_xor(dsum, 4);
@@ -160,12 +194,10 @@ __global__ void __launch_bounds__(256) otf_bwd_wt_kernel(OtfBwdParams p) {
   }
 }
 
-// Projection as the forward computes it, rounded to fp16 as there: X_lat^T = W^T X^T with
-// A = W^T rows and B = raw X rows (K: the forward's own operand order; V: the forward's
-// V_lat = V WV with A and B swapped, which v_mfma_f32_16x16x32_bf16 computes bit for bit as
-// the transpose), four k-steps of 32 input dims each.  Block = 256 keys of one (b, h); waves
+// Projection for the dQ kernel, rounded to fp16: X_lat^T = W^T X^T with A = W^T rows and
+// B = raw X rows, four k-steps of 32 input dims each.  Block = 256 keys of one (b, h); waves
 // 0-1 project K, waves 2-3 V, each taking every other 16-key block with the next block's rows
-// loaded while the current one is multiplied.  Grid (Skp / 256 rounded up, H, B).
+// loaded while the current one is multiplied.  Grid (H, Skp / 256 rounded up, B).
 __global__ void __launch_bounds__(256) otf_bwd_proj_kernel(OtfBwdParams p) {
   // Heads fastest in the grid: workgroups issued together read neighbouring 256-byte pieces of
   // the same [B, S, H, 128] rows (the 16 key blocks of one head lie 8 KB apart per key).
@@ -215,35 +247,88 @@ __global__ void __launch_bounds__(256) otf_bwd_proj_kernel(OtfBwdParams p) {
   }
 }
 
+// X_lat * mul of keys k0 + 16 kb + l16 (kb = 0, 1) as bf16 pairs (hi, lo), each in the layout
+// of an MFMA B operand whose k index runs over dims 32 ks + 8 g .. +7 (lane l, g = l/16).
+// Projected here from the raw rows: X_lat^T = W^T X^T over four k-steps of 32 input dims.  A C
+// tile's lane holds four consecutive rows 4 g .. 4 g + 3, so the A operand (W^T rows) is taken
+// in the row order pi(ks, half, 4 g' + i) = 32 ks + 8 g' + 4 half + i: the C tiles of halves
+// 0 and 1 then hold dims 32 ks + 8 g + 0..3 and + 4..7 of each lane's key, the two halves of
+// its B operand.  Keys at or past Sk come out zero.
+__device__ __forceinline__ void project_keys(const OtfBwdParams& p, int x, int b, int h, int k0, int lane,
+                                             bf16x8 (&hi)[2][2], bf16x8 (&lo)[2][2]) {
+  const int l16 = lane & 15, g = lane >> 4;
+  const bf16* src = x ? p.v + b * p.v_sb + h * p.v_sh : p.k + b * p.k_sb + h * p.k_sh;
+  const int64_t ss = x ? p.v_ss : p.k_ss;
+  bf16x8 xr[2][4];   // [kb][s]: X[key k0 + 16 kb + l16][32 s + 8 g ..]
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int gk = min(k0 + 16 * kb + l16, p.Sk - 1);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xr[kb][s] = *reinterpret_cast<const bf16x8*>(src + (int64_t)gk * ss + 32 * s + 8 * g);
+  }
+  const bf16* wt = p.wt + ((size_t)x * p.H + h) * (kLat * kIn) + (8 * (l16 >> 2) + (l16 & 3)) * kIn + 8 * g;
+  f32x4 c[2][2][2];   // [ks][half][kb]
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      c[ks][half][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      c[ks][half][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(wt + (32 * ks + 4 * half) * kIn + 32 * s);
+        c[ks][half][0] = mfma_bf16(a, xr[0][s], c[ks][half][0]);
+        c[ks][half][1] = mfma_bf16(a, xr[1][s], c[ks][half][1]);
+      }
+    }
+  const float mul = x ? 1.f : p.scale_log2;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const bool live = k0 + 16 * kb + l16 < p.Sk;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      float v[8];
+      __bf16 vh[8], vl[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[i] = live ? c[ks][0][kb][i] * mul : 0.f;
+        v[4 + i] = live ? c[ks][1][kb][i] * mul : 0.f;
+      }
+      split_bf16_rn(v, vh, vl);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        hi[kb][ks][j] = vh[j];
+        lo[kb][ks][j] = vl[j];
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
-// dK_lat / dV_lat: block = 128 keys of one (b, h), wave w owns keys k0 = 128 kblk + 32 w .. +31.
-// Rows stream in stages of 64 (Q and dO as fp16, copied global -> LDS one stage ahead), from
-// the first row that sees any of the block's keys.  Per 32-row sub-tile and wave:
-//   S  = Q K_lat^T, dP = dO V_lat^T    (A = Q / dO rows from LDS, B = K_lat / V_lat in registers)
-//   P  = exp2(S scale log2e - lse2), dS = P (dP - D)   (K_lat stored times scale log2e; the S
-//        accumulators start at -lse2, so the product is the exp2 argument)
-//   dV_lat^T += dO^T P, dK_lat^T += Q^T dS   (A = dO^T / Q^T by transposed reads; B = P / dS
-//                                           straight from the C tiles of S and dP)
+// dK_lat / dV_lat: block = 128 keys of one (b, h), wave w owns keys k0 = 128 kblk + 32 w .. +31,
+// whose K_lat (times scale log2 e) and V_lat it projects into registers as bf16 pairs.  Rows
+// stream in stages of 64 (Q and dO rows as they are, bf16, copied global -> LDS one stage ahead),
+// from the first row that sees any of the block's keys.  Per 32-row sub-tile and wave:
+//   S  = Q K_lat^T, dP = dO V_lat^T    (A = Q / dO rows from LDS, B = hi and lo in registers:
+//                                      four MFMAs per 16 x 16 tile)
+//   P  = exp2(S - lse2), dS = P (dP - D)   (the S accumulators start at -lse2 and the dP ones at
+//        -D, so the products hand over the exp2 argument and dP - D)
+//   dV_lat^T += dO^T (P_hi + P_lo), dK_lat^T += Q^T (dS_hi + dS_lo)
+//                                      (A = dO^T / Q^T by transposed reads; B = the C tiles of
+//                                      S and dP as they are)
 // Grid: key blocks heavy first (block 0 sees every row under the causal mask).
 __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
-  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kRowStage];
   DMLA_LDS char* lds = (DMLA_LDS char*)smem;
   const int wave = uniform(threadIdx.x >> 6), lane = lane_id(), l16 = lane & 15, g = lane >> 4;
   const int BH = p.B * p.H;
   const int bh = (int)blockIdx.x % BH, kblk = (int)blockIdx.x / BH;
+  const int b = bh / p.H, h = bh % p.H;
   const int off = p.Sk - p.Sq;
   const int k0 = kblk * kKeyBlk + 32 * wave;
-  f16x8 kreg[2][2], vreg[2][2];   // [kb][ks]: X_lat[k0 + 16 kb + l16][32 ks + 8 g ..]
-  {
-    const size_t base = ((size_t)bh * p.Skp + k0 + l16) * kLat + 8 * g;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        kreg[kb][ks] = *reinterpret_cast<const f16x8*>(p.klat + base + 16 * kb * kLat + 32 * ks);
-        vreg[kb][ks] = *reinterpret_cast<const f16x8*>(p.vlat + base + 16 * kb * kLat + 32 * ks);
-      }
-  }
+  bf16x8 khi[2][2], klo[2][2], vhi[2][2], vlo[2][2];   // [kb][ks]
+  project_keys(p, 0, b, h, k0, lane, khi, klo);
+  project_keys(p, 1, b, h, k0, lane, vhi, vlo);
   f32x4 dkt[4][2], dvt[4][2];     // [db][kb]: X_lat^T[dim 16 db + 4 g + i][key k0 + 16 kb + l16]
 #pragma unroll
   for (int db = 0; db < 4; ++db)
@@ -255,58 +340,76 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
   const int row_first = p.causal ? max(0, kblk * kKeyBlk - off) : 0;
   const int rs0 = row_first / 64 * 64;
   const int n_st = row_first >= p.Sq ? 0 : (p.Sq - rs0 + 63) / 64;
-  const _Float16* qsrc = p.q16 + (size_t)bh * p.Sqp * kLat;
-  const _Float16* dsrc = p.do16 + (size_t)bh * p.Sqp * kLat;
+  const bf16* qsrc = p.q + b * p.q_sb + h * p.q_sh;
+  const bf16* dsrc = p.dout + b * p.do_sb + h * p.do_sh;
   const float* lse2 = p.lse2 + (size_t)bh * p.Sqp;
   const float* nd = p.nd + (size_t)bh * p.Sqp;
   const unsigned lbase = lds_addr(lds);
 
+  // Rows row0 .. row0+63 of Q and dO (stage_pair) and of lse2 and -D (waves 0 and 1, one
+  // 4-byte copy per lane) into the stage at byte address lst.
+  auto stage_rows = [&](int row0, unsigned lst) {
+    stage_pair(qsrc, p.q_ss, dsrc, p.do_ss, row0, p.Sq, lst, wave, lane);
+    if (wave < 2) dma4(wave ? nd : lse2, 4u * (unsigned)(row0 + lane), lst + kStage + 256 * wave);
+  };
+
   // One 32-row sub-tile; kMask applies the causal / key-range mask (only sub-tiles that reach
-  // past some pair's limit need it), so the common case is straight-line code.
-  // dP - D comes straight out of the dP product: its accumulator starts at -D of the row.
-  auto subtile = [&](const DMLA_LDS char* qt, const DMLA_LDS char* dt, int r0, const f32x4 (&ls)[2],
-                     const f32x4 (&ndv)[2], auto mask_tag) {
+  // past some pair's limit need it), so the common case is straight-line code.  rs points at
+  // the stage's lse2 and -D of the sub-tile's rows.
+  auto subtile = [&](const DMLA_LDS char* qt, const DMLA_LDS char* dt, const DMLA_LDS char* rs, int r0,
+                     auto mask_tag) {
     constexpr bool kMask = decltype(mask_tag)::value;
     f32x4 sacc[2][2], dpacc[2][2];   // [rb][kb]: rows 16 rb + 4 g + i, key 16 kb + l16
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-      const f16x8 qa0 = lds_f16x8(qt + row_operand_off(lane, rb, 0));
-      const f16x8 qa1 = lds_f16x8(qt + row_operand_off(lane, rb, 1));
-      const f16x8 oa0 = lds_f16x8(dt + row_operand_off(lane, rb, 0));
-      const f16x8 oa1 = lds_f16x8(dt + row_operand_off(lane, rb, 1));
+      const f32x4 ls = *reinterpret_cast<const DMLA_LDS f32x4*>(rs + 4 * (16 * rb + 4 * g));
+      const f32x4 ndv = *reinterpret_cast<const DMLA_LDS f32x4*>(rs + 256 + 4 * (16 * rb + 4 * g));
+      const bf16x8 qa0 = lds_bf16x8(qt + row_operand_off(lane, rb, 0));
+      const bf16x8 qa1 = lds_bf16x8(qt + row_operand_off(lane, rb, 1));
+      const bf16x8 oa0 = lds_bf16x8(dt + row_operand_off(lane, rb, 0));
+      const bf16x8 oa1 = lds_bf16x8(dt + row_operand_off(lane, rb, 1));
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        sacc[rb][kb] = mfma_f16(qa0, kreg[kb][0], -ls[rb]);   // S log2(e) scale - lse2
-        sacc[rb][kb] = mfma_f16(qa1, kreg[kb][1], sacc[rb][kb]);
-        dpacc[rb][kb] = mfma_f16(oa0, vreg[kb][0], ndv[rb]);
-        dpacc[rb][kb] = mfma_f16(oa1, vreg[kb][1], dpacc[rb][kb]);
+        f32x4 s = mfma_bf16(qa0, klo[kb][0], -ls);
+        s = mfma_bf16(qa0, khi[kb][0], s);
+        s = mfma_bf16(qa1, klo[kb][1], s);
+        sacc[rb][kb] = mfma_bf16(qa1, khi[kb][1], s);
+        f32x4 d = mfma_bf16(oa0, vlo[kb][0], ndv);
+        d = mfma_bf16(oa0, vhi[kb][0], d);
+        d = mfma_bf16(oa1, vlo[kb][1], d);
+        dpacc[rb][kb] = mfma_bf16(oa1, vhi[kb][1], d);
       }
     }
-    f16x8 pb[2], dsb[2];   // [kb]: B operands, slot 4 rb + i = row 16 rb + 4 g + i
+    bf16x8 pbh[2], pbl[2], dsh[2], dsl[2];   // [kb]: B operands, slot 4 rb + i = row 16 rb + 4 g + i
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
+    for (int kb = 0; kb < 2; ++kb) {
+      float pv[8], dv[8];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float pv = fast_exp2(sacc[rb][kb][i]);
+          float e = fast_exp2(sacc[rb][kb][i]);
           if constexpr (kMask) {
             const int row = r0 + 16 * rb + 4 * g + i, key = k0 + 16 * kb + l16;
             const int lim = p.causal ? min(row + off, p.Sk - 1) : p.Sk - 1;
-            pv = key > lim ? 0.f : pv;
+            e = key > lim ? 0.f : e;
           }
-          pb[kb][4 * rb + i] = (_Float16)pv;
-          dsb[kb][4 * rb + i] = (_Float16)(pv * dpacc[rb][kb][i]);
+          pv[4 * rb + i] = e;
+          dv[4 * rb + i] = e * dpacc[rb][kb][i];
         }
+      split_bf16(pv, pbh[kb], pbl[kb]);
+      split_bf16(dv, dsh[kb], dsl[kb]);
     }
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const f16x8 ot = lds_col_operand(dt, lane, db);   // dO^T[dim 16 db + l16][rows]
-      const f16x8 qtt = lds_col_operand(qt, lane, db);  // Q^T
+      const bf16x8 ot = lds_col_operand_bf(dt, lane, db);   // dO^T[dim 16 db + l16][rows]
+      const bf16x8 qtt = lds_col_operand_bf(qt, lane, db);  // Q^T
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        dvt[db][kb] = mfma_f16(ot, pb[kb], dvt[db][kb]);
-        dkt[db][kb] = mfma_f16(qtt, dsb[kb], dkt[db][kb]);
+        dvt[db][kb] = mfma_bf16(ot, pbl[kb], dvt[db][kb]);
+        dvt[db][kb] = mfma_bf16(ot, pbh[kb], dvt[db][kb]);
+        dkt[db][kb] = mfma_bf16(qtt, dsl[kb], dkt[db][kb]);
+        dkt[db][kb] = mfma_bf16(qtt, dsh[kb], dkt[db][kb]);
       }
     }
   };
@@ -317,55 +420,60 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
     constexpr int kBuf = decltype(buf_tag)::value;
     wait_vmem();
     __syncthreads();   // stage s complete; every wave is done with stage s-1
-    // lse2 and -D of rows r0 + 16 rb + 4 g + i, loaded before the next stage's copies so that
-    // waiting for them does not wait for the copies.
-    f32x4 ls[2][2], ndv[2][2];   // [t][rb]
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        const int r = rs0 + 64 * s + 32 * t + 16 * rb + 4 * g;
-        ls[t][rb] = *reinterpret_cast<const f32x4*>(lse2 + r);
-        ndv[t][rb] = *reinterpret_cast<const f32x4*>(nd + r);
-      }
-    if (s + 1 < n_st) stage_pair(qsrc, dsrc, rs0 + 64 * (s + 1), lbase + (1 - kBuf) * kStage, wave, lane);
-    const DMLA_LDS char* st = lds + kBuf * kStage;
+    if (s + 1 < n_st) stage_rows(rs0 + 64 * (s + 1), lbase + (1 - kBuf) * kRowStage);
+    const DMLA_LDS char* st = lds + kBuf * kRowStage;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int r0 = rs0 + 64 * s + 32 * t;
       if (r0 >= p.Sq || (p.causal && k0 > r0 + 31 + off)) continue;   // padding only / all masked
       if (k0 + 31 >= p.Sk || (p.causal && k0 + 31 > r0 + off))
-        subtile(st + t * kTile, st + (2 + t) * kTile, r0, ls[t], ndv[t], std::true_type{});
+        subtile(st + t * kTile, st + (2 + t) * kTile, st + kStage + 128 * t, r0, std::true_type{});
       else
-        subtile(st + t * kTile, st + (2 + t) * kTile, r0, ls[t], ndv[t], std::false_type{});
+        subtile(st + t * kTile, st + (2 + t) * kTile, st + kStage + 128 * t, r0, std::false_type{});
     }
   };
-  if (n_st > 0) stage_pair(qsrc, dsrc, rs0, lbase, wave, lane);
+  if (n_st > 0) stage_rows(rs0, lbase);
   for (int s = 0; s < n_st; s += 2) {
     stage_iter(s, std::integral_constant<int, 0>{});
     if (s + 1 < n_st) stage_iter(s + 1, std::integral_constant<int, 1>{});
   }
-  // dK_lat = scale dS^T Q and dV_lat = P^T dO as fp16 rows (keys past Sk hold zeros: P = 0 there)
+  // dK_lat = scale dS^T Q and dV_lat = P^T dO as bf16 hi / lo planes (keys past Sk hold zeros:
+  // P = 0 there)
+  const size_t plane = (size_t)BH * p.Skp * kLat;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
-    const size_t row = ((size_t)bh * p.Skp + k0 + 16 * kb + l16) * kLat;
+    bf16* row = p.dxlat + ((size_t)bh * p.Skp + k0 + 16 * kb + l16) * kLat + 4 * g;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      f16x4 a, c;
+      float a[4], c[4];
+      __bf16 ah[4], al[4], ch[4], cl[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        a[i] = (_Float16)(dkt[db][kb][i] * p.scale);
-        c[i] = (_Float16)dvt[db][kb][i];
+        a[i] = dkt[db][kb][i] * p.scale;
+        c[i] = dvt[db][kb][i];
       }
-      *reinterpret_cast<f16x4*>(p.dklat + row + 16 * db + 4 * g) = a;
-      *reinterpret_cast<f16x4*>(p.dvlat + row + 16 * db + 4 * g) = c;
+      split_bf16_rn(a, ah, al);
+      split_bf16_rn(c, ch, cl);
+      bf16x4 vah, val, vch, vcl;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        vah[i] = ah[i];
+        val[i] = al[i];
+        vch[i] = ch[i];
+        vcl[i] = cl[i];
+      }
+      *reinterpret_cast<bf16x4*>(row + 16 * db) = vah;
+      *reinterpret_cast<bf16x4*>(row + plane + 16 * db) = val;
+      *reinterpret_cast<bf16x4*>(row + 2 * plane + 16 * db) = vch;
+      *reinterpret_cast<bf16x4*>(row + 3 * plane + 16 * db) = vcl;
     }
   }
 }
 
 // ---------------------------------------------------------------------------------------------
-// dQ: block = 128 rows of one (b, h), wave w owns rows r0 = 128 rblk + 32 w .. +31.  Keys stream
-// in stages of 64 (K_lat and V_lat, copied one stage ahead) up to the last key any row sees.
+// dQ: block = 128 rows of one (b, h), wave w owns rows r0 = 128 rblk + 32 w .. +31, whose Q and
+// dO it holds in registers as fp16 (converted exactly from bf16).  Keys stream in stages of 64
+// (fp16 K_lat and V_lat, copied one stage ahead) up to the last key any row sees.
 // Per 32-key sub-tile and wave:
 //   S^T = K_lat Q^T, dP^T = V_lat dO^T   (A = K_lat / V_lat rows from LDS, B = Q / dO in registers)
 //   dS^T = P^T (dP^T - D)
@@ -382,16 +490,19 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
   const int b = bh / p.H, h = bh % p.H;
   const int off = p.Sk - p.Sq;
   const int r0 = rblk * kRowBlk + 32 * wave;
-  f16x8 qreg[2][2], oreg[2][2];   // [rb][ks]: X16[r0 + 16 rb + l16][32 ks + 8 g ..]
+  f16x8 qreg[2][2], oreg[2][2];   // [rb][ks]: X[r0 + 16 rb + l16][32 ks + 8 g ..] as fp16
   float lse[2];
   f32x4 ndv[2];   // -D of row r0 + 16 rb + l16 in all four elements: the dP^T accumulator start
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
-    const size_t base = ((size_t)bh * p.Sqp + r0 + 16 * rb + l16) * kLat + 8 * g;
+    // Rows past Sq re-read row Sq-1: their lse2 is +inf, so their P is 0.
+    const int row = min(r0 + 16 * rb + l16, p.Sq - 1);
+    const bf16* qrow = p.q + b * p.q_sb + h * p.q_sh + (int64_t)row * p.q_ss + 8 * g;
+    const bf16* orow = p.dout + b * p.do_sb + h * p.do_sh + (int64_t)row * p.do_ss + 8 * g;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      qreg[rb][ks] = *reinterpret_cast<const f16x8*>(p.q16 + base + 32 * ks);
-      oreg[rb][ks] = *reinterpret_cast<const f16x8*>(p.do16 + base + 32 * ks);
+      qreg[rb][ks] = to_f16(*reinterpret_cast<const bf16x8*>(qrow + 32 * ks));
+      oreg[rb][ks] = to_f16(*reinterpret_cast<const bf16x8*>(orow + 32 * ks));
     }
     lse[rb] = p.lse2[(size_t)bh * p.Sqp + r0 + 16 * rb + l16];
     const float n = p.nd[(size_t)bh * p.Sqp + r0 + 16 * rb + l16];
@@ -454,7 +565,7 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
     constexpr int kBuf = decltype(buf_tag)::value;
     wait_vmem();
     __syncthreads();
-    if (s + 1 < n_st) stage_pair(ksrc, vsrc, 64 * (s + 1), lbase + (1 - kBuf) * kStage, wave, lane);
+    if (s + 1 < n_st) stage_pair(ksrc, kLat, vsrc, kLat, 64 * (s + 1), p.Skp, lbase + (1 - kBuf) * kStage, wave, lane);
     const DMLA_LDS char* st = lds + kBuf * kStage;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -466,7 +577,7 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
         subtile(st + t * kTile, st + (2 + t) * kTile, c0, std::false_type{});
     }
   };
-  if (n_st > 0) stage_pair(ksrc, vsrc, 0, lbase, wave, lane);
+  if (n_st > 0) stage_pair(ksrc, kLat, vsrc, kLat, 0, p.Skp, lbase, wave, lane);
   for (int s = 0; s < n_st; s += 2) {
     stage_iter(s, std::integral_constant<int, 0>{});
     if (s + 1 < n_st) stage_iter(s + 1, std::integral_constant<int, 1>{});
@@ -477,22 +588,26 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
     for (int i = 0; i < 4; ++i) {
       const int row = r0 + 16 * rb + 4 * g + i;
       if (row >= p.Sq) continue;
-      bf16* out = p.dq + b * p.dq_sb + h * p.dq_sh + (int64_t)row * p.dq_ss + l16;
+      const int64_t at = b * p.dq_sb + h * p.dq_sh + (int64_t)row * p.dq_ss + l16;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) out[16 * db] = (bf16)(dq[rb][db][i] * kLn2);   // scale / (scale log2 e)
+      for (int db = 0; db < 4; ++db) {
+        const float v = dq[rb][db][i] * kLn2;   // scale / (scale log2 e)
+        if (p.dq_fp32) static_cast<float*>(p.dq)[at + 16 * db] = v;
+        else static_cast<bf16*>(p.dq)[at + 16 * db] = (bf16)v;
+      }
     }
 }
 
 // ---------------------------------------------------------------------------------------------
 // Weight side: block = (tensor x in {K, V}, head h, batch b, chunk c of 1024 keys), grid
-// (n_sc, H, 2 B).  Per 64-key block (raw X as fp16 through registers, dX_lat copied directly,
-// both one block ahead):
+// (n_sc, H, 2 B).  Per 64-key block (raw X rows and the dX_lat hi / lo planes copied global ->
+// LDS directly, one block ahead):
 //   dX^T[in][key] = W[in][:] dX_lat^T       wave w: keys 16 w .. +15 (A = W rows in registers,
-//                                           B = dX_lat rows from LDS); written as bf16 rows of dX
+//                                           B = dX_lat hi, lo rows from LDS); written as dX rows
 //   dW[in][dim]  += X^T[in][key] dX_lat     wave w: input dims 32 w .. +31 (both operands by
 //                                           transposed reads, keys in the same order)
 // The fp32 dW partial of the chunk goes to wpart; otf_bwd_wreduce_kernel sums the chunks.
-__global__ void __launch_bounds__(256) otf_bwd_wgrad_kernel(OtfBwdParams p) {
+__global__ void __launch_bounds__(256, 2) otf_bwd_wgrad_kernel(OtfBwdParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[2 * kWgStage];
   DMLA_LDS char* lds = (DMLA_LDS char*)smem;
   const int wave = uniform(threadIdx.x >> 6), lane = lane_id(), l16 = lane & 15, g = lane >> 4;
@@ -501,101 +616,101 @@ __global__ void __launch_bounds__(256) otf_bwd_wgrad_kernel(OtfBwdParams p) {
   const bf16* X = x ? p.v + b * p.v_sb + h * p.v_sh : p.k + b * p.k_sb + h * p.k_sh;
   const int64_t x_ss = x ? p.v_ss : p.k_ss;
   const bf16* W = (x ? p.wv : p.wk) + h * p.w_sh;
-  const _Float16* dxl = (x ? p.dvlat : p.dklat) + (size_t)bh * p.Skp * kLat;
-  bf16* dX = (x ? p.dv : p.dk) + b * p.dk_sb + h * p.dk_sh;
+  const size_t plane = (size_t)p.B * p.H * p.Skp * kLat;
+  const bf16* dxh = p.dxlat + 2 * x * plane + (size_t)bh * p.Skp * kLat;
+  const bf16* dxl = dxh + plane;
+  const int64_t dx_at = b * p.dk_sb + h * p.dk_sh;
   const int key_lo = c * kChunk, key_hi = min(p.Sk, key_lo + kChunk);
   const int n_blk = (key_hi - key_lo + 63) / 64;
   const unsigned lbase = lds_addr(lds);
 
-  f16x8 wa[8][2];   // [ib][ks]: W[16 ib + l16][32 ks + 8 g ..]
+  bf16x8 wa[8][2];   // [ib][ks]: W[16 ib + l16][32 ks + 8 g ..]
 #pragma unroll
   for (int ib = 0; ib < 8; ++ib)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-      wa[ib][ks] = to_f16(*reinterpret_cast<const bf16x8*>(W + (16 * ib + l16) * p.w_si + 32 * ks + 8 * g));
+    for (int ks = 0; ks < 2; ++ks) wa[ib][ks] = *reinterpret_cast<const bf16x8*>(W + (16 * ib + l16) * p.w_si + 32 * ks + 8 * g);
   f32x4 dw[2][4];   // [ib - 2 w][db]: dW[16 ib + 4 g + i][16 db + l16]
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
     for (int db = 0; db < 4; ++db) dw[a][db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Raw X block: 64 keys x 16 chunks of 16 B, four chunks per thread (q = tid + 256 j).
-  bf16x8 xr[4];
-  auto load_x = [&](int blk) {
+  // One 64-key block into stage buffer buf: raw X as two 32-key tiles of two chunk groups
+  // (16 wave copies of 1 KB), then the hi and lo dX_lat planes as two 32-key tiles each
+  // (16 copies); eight per wave.  Keys past Sk re-read key Sk-1 (their dX_lat rows are zero).
+  auto stage_block = [&](int blk, int buf) {
+    const int key0 = key_lo + 64 * blk;
+    const unsigned sbuf = lbase + buf * kWgStage;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int q = threadIdx.x + 256 * j;
-      const int gk = min(key_lo + 64 * blk + (q >> 4), p.Sk - 1);
-      xr[j] = *reinterpret_cast<const bf16x8*>(X + (int64_t)gk * x_ss + 8 * (q & 15));
-    }
-  };
-  auto put_x = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int q = threadIdx.x + 256 * j;
-      const int kk = q >> 4, ch = q & 15;
-      *reinterpret_cast<DMLA_LDS f16x8*>(lds + buf * kWgStage + (kk >> 5) * kXTile + tile_chunk_off(kk & 31, ch)) =
-          to_f16(xr[j]);
-    }
-  };
-  // dX_lat block: 8 KB as two 32-key tiles, eight 1 KB wave copies, two per wave.
-  auto dma_dxl = [&](int blk, int buf) {
-#pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
-      const int n = 2 * wave + cc;
-      const int t = n >> 2, part = n & 3;
+    for (int cc = 0; cc < 4; ++cc) {
+      const int n = 4 * wave + cc;
+      const int t = n >> 3, grp = (n >> 2) & 1, part = n & 3;
       const int row = 8 * part + (lane >> 3);
       const int lc = (lane & 7) ^ swz(row & 15);
-      const unsigned voff = 2u * (unsigned)((key_lo + 64 * blk + 32 * t + row) * kLat + 8 * lc);
-      dma16(dxl, voff, lbase + buf * kWgStage + 2 * kXTile + t * kTile + part * 1024);
+      const int rel = min(key0 + 32 * t + row, p.Sk - 1) - key0;
+      dma16(X + key0 * x_ss, 2u * (unsigned)(rel * x_ss + 64 * grp + 8 * lc), sbuf + t * kXTile + grp * kGroupBytes + part * 1024);
+    }
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const int n = 4 * wave + cc;
+      const int pl = n >> 3, t = (n >> 2) & 1, part = n & 3;
+      const int row = 8 * part + (lane >> 3);
+      const int lc = (lane & 7) ^ swz(row & 15);
+      dma16(pl ? dxl : dxh, 2u * (unsigned)((key0 + 32 * t + row) * kLat + 8 * lc),
+            sbuf + 2 * kXTile + (2 * pl + t) * kTile + part * 1024);
     }
   };
 
-  if (n_blk > 0) {
-    load_x(0);
-    dma_dxl(0, 0);
-    put_x(0);
-  }
+  if (n_blk > 0) stage_block(0, 0);
   for (int blk = 0; blk < n_blk; ++blk) {
     wait_vmem();
     __syncthreads();   // block blk complete in buffer blk & 1; buffer (blk + 1) & 1 free
-    if (blk + 1 < n_blk) {
-      load_x(blk + 1);
-      dma_dxl(blk + 1, (blk + 1) & 1);
-    }
+    if (blk + 1 < n_blk) stage_block(blk + 1, (blk + 1) & 1);
     const DMLA_LDS char* xs = lds + (blk & 1) * kWgStage;
-    const DMLA_LDS char* ds = xs + 2 * kXTile;
+    const DMLA_LDS char* dhs = xs + 2 * kXTile;     // hi tiles (keys 0-31, 32-63)
+    const DMLA_LDS char* dls = dhs + 2 * kTile;     // lo tiles
     // dX^T for keys 16 wave + l16 of the block
     {
-      const DMLA_LDS char* dt = ds + (wave >> 1) * kTile;
-      const f16x8 b0 = lds_f16x8(dt + row_operand_off(lane, wave & 1, 0));
-      const f16x8 b1 = lds_f16x8(dt + row_operand_off(lane, wave & 1, 1));
+      const int tt = (wave >> 1) * kTile, rb = wave & 1;
+      const bf16x8 h0 = lds_bf16x8(dhs + tt + row_operand_off(lane, rb, 0));
+      const bf16x8 h1 = lds_bf16x8(dhs + tt + row_operand_off(lane, rb, 1));
+      const bf16x8 lo0 = lds_bf16x8(dls + tt + row_operand_off(lane, rb, 0));
+      const bf16x8 lo1 = lds_bf16x8(dls + tt + row_operand_off(lane, rb, 1));
       const int key = key_lo + 64 * blk + 16 * wave + l16;
 #pragma unroll
       for (int ib = 0; ib < 8; ++ib) {
-        f32x4 cacc = mfma_f16(wa[ib][0], b0, f32x4{0.f, 0.f, 0.f, 0.f});
-        cacc = mfma_f16(wa[ib][1], b1, cacc);    // dX^T[in 16 ib + 4 g + i][key]
+        f32x4 cacc = mfma_bf16(wa[ib][0], lo0, f32x4{0.f, 0.f, 0.f, 0.f});
+        cacc = mfma_bf16(wa[ib][0], h0, cacc);
+        cacc = mfma_bf16(wa[ib][1], lo1, cacc);
+        cacc = mfma_bf16(wa[ib][1], h1, cacc);    // dX^T[in 16 ib + 4 g + i][key]
         if (key < key_hi) {
-          bf16x4 v;
+          const int64_t at = dx_at + (int64_t)key * p.dk_ss + 16 * ib + 4 * g;
+          if (p.dkv_fp32) {
+            *reinterpret_cast<f32x4*>(static_cast<float*>(x ? p.dv : p.dk) + at) = cacc;
+          } else {
+            bf16x4 v;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) v[i] = (bf16)cacc[i];
-          *reinterpret_cast<bf16x4*>(dX + (int64_t)key * p.dk_ss + 16 * ib + 4 * g) = v;
+            for (int i = 0; i < 4; ++i) v[i] = (bf16)cacc[i];
+            *reinterpret_cast<bf16x4*>(static_cast<bf16*>(x ? p.dv : p.dk) + at) = v;
+          }
         }
       }
     }
     // dW over the block's 64 keys (two k-steps of 32)
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const f16x8 a0 = lds_col_operand(xs + t * kXTile, lane, 2 * wave);
-      const f16x8 a1 = lds_col_operand(xs + t * kXTile, lane, 2 * wave + 1);
+      const bf16x8 a0 = lds_col_operand_bf(xs + t * kXTile, lane, 2 * wave);
+      const bf16x8 a1 = lds_col_operand_bf(xs + t * kXTile, lane, 2 * wave + 1);
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const f16x8 bm = lds_col_operand(ds + t * kTile, lane, db);
-        dw[0][db] = mfma_f16(a0, bm, dw[0][db]);
-        dw[1][db] = mfma_f16(a1, bm, dw[1][db]);
+        const bf16x8 bl = lds_col_operand_bf(dls + t * kTile, lane, db);
+        const bf16x8 bh2 = lds_col_operand_bf(dhs + t * kTile, lane, db);
+        dw[0][db] = mfma_bf16(a0, bl, dw[0][db]);
+        dw[0][db] = mfma_bf16(a0, bh2, dw[0][db]);
+        dw[1][db] = mfma_bf16(a1, bl, dw[1][db]);
+        dw[1][db] = mfma_bf16(a1, bh2, dw[1][db]);
       }
     }
-    if (blk + 1 < n_blk) put_x((blk + 1) & 1);
   }
   float* part = p.wpart + (((size_t)x * p.H + h) * ((size_t)p.B * p.n_sc) + (size_t)b * p.n_sc + c) * (kIn * kLat);
 #pragma unroll
@@ -622,7 +737,7 @@ __global__ void __launch_bounds__(256) otf_bwd_wreduce_kernel(OtfBwdParams p) {
 
 struct OtfBwdPlan {
   int Sqp, Skp, n_sc;
-  size_t off_q16, off_do16, off_lse2, off_nd, off_klat, off_vlat, off_dklat, off_dvlat, off_wpart, off_wt, bytes;
+  size_t off_lse2, off_nd, off_klat, off_vlat, off_dx, off_wpart, off_wt, bytes;
 };
 
 OtfBwdPlan make_otf_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk) {
@@ -633,21 +748,19 @@ OtfBwdPlan make_otf_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk) {
   auto up = [](size_t n) { return (n + 255) / 256 * 256; };
   const size_t rows = (size_t)B * H * pl.Sqp, keys = (size_t)B * H * pl.Skp;
   size_t o = 0;
-  pl.off_q16 = o;   o += up(rows * kLat * 2);
-  pl.off_do16 = o;  o += up(rows * kLat * 2);
   pl.off_lse2 = o;  o += up(rows * sizeof(float));
   pl.off_nd = o;    o += up(rows * sizeof(float));
   pl.off_klat = o;  o += up(keys * kLat * 2);
   pl.off_vlat = o;  o += up(keys * kLat * 2);
-  pl.off_dklat = o; o += up(keys * kLat * 2);
-  pl.off_dvlat = o; o += up(keys * kLat * 2);
+  pl.off_dx = o;    o += up(4 * keys * kLat * 2);
   pl.off_wpart = o; o += up((size_t)2 * H * B * pl.n_sc * kIn * kLat * sizeof(float));
   pl.off_wt = o;    o += up((size_t)2 * H * kIn * kLat * 2);
   pl.bytes = o;
   return pl;
 }
 
-constexpr int64_t kOtfBwdMaxSeq = (int64_t)1 << 24;   // keeps the 32-bit copy offsets in range
+constexpr int64_t kOtfBwdMaxSeq = (int64_t)1 << 24;    // keeps the 32-bit copy offsets in range
+constexpr int64_t kOtfBwdMaxRowStride = (int64_t)1 << 24;   // q / dout / k / v row strides (elements)
 
 }  // namespace
 }  // namespace dmla
@@ -669,8 +782,9 @@ extern "C" int dmla_bwd_onthefly(const void* q, const void* k, const void* v, co
                                  int64_t v_ss, int64_t v_sh, int64_t w_sh, int64_t w_si, int64_t o_sb,
                                  int64_t o_sh, int64_t o_ss, int64_t do_sb, int64_t do_sh, int64_t do_ss,
                                  int64_t dq_sb, int64_t dq_sh, int64_t dq_ss, int64_t dk_sb, int64_t dk_ss,
-                                 int64_t dk_sh, int64_t dw_sh, int64_t dw_si, int dw_fp32, float softmax_scale,
-                                 int causal, void* workspace, int64_t workspace_bytes, dmla_stream_t stream) {
+                                 int64_t dk_sh, int64_t dw_sh, int64_t dw_si, int dq_fp32, int dkv_fp32,
+                                 int dw_fp32, float softmax_scale, int causal, void* workspace,
+                                 int64_t workspace_bytes, dmla_stream_t stream) {
   clear_error();
   if (!q || !k || !v || !wk || !wv || !o || !dout || !m || !l || !dq || !dk || !dv || !dwk || !dwv)
     return fail(DMLA_ERR_INVALID_ARG, "dmla_bwd_onthefly: null pointer argument");
@@ -689,6 +803,9 @@ extern "C" int dmla_bwd_onthefly(const void* q, const void* k, const void* v, co
       !mult8(o_sh) || !mult8(o_ss) || !mult8(do_sb) || !mult8(do_sh) || !mult8(do_ss) || !mult8(dk_sb) ||
       !mult8(dk_ss) || !mult8(dk_sh))
     return fail(DMLA_ERR_INVALID_ARG, "dmla_bwd_onthefly: strides must be multiples of 8 elements");
+  if (q_ss < 0 || do_ss < 0 || k_ss < 0 || v_ss < 0 || q_ss >= kOtfBwdMaxRowStride || do_ss >= kOtfBwdMaxRowStride ||
+      k_ss >= kOtfBwdMaxRowStride || v_ss >= kOtfBwdMaxRowStride)
+    return fail(DMLA_ERR_UNSUPPORTED, "dmla_bwd_onthefly: row strides of q, dout, k and v must be in [0, 2^24)");
   if (Sq > kOtfBwdMaxSeq || Sk > kOtfBwdMaxSeq)
     return fail(DMLA_ERR_UNSUPPORTED, "dmla_bwd_onthefly: Sq and Sk must be at most 2^24");
   if (B == 0 || H == 0) return DMLA_OK;
@@ -713,11 +830,13 @@ extern "C" int dmla_bwd_onthefly(const void* q, const void* k, const void* v, co
   p.dout = static_cast<const bf16*>(dout);
   p.m = m;
   p.l = l;
-  p.dq = static_cast<bf16*>(dq);
-  p.dk = static_cast<bf16*>(dk);
-  p.dv = static_cast<bf16*>(dv);
+  p.dq = dq;
+  p.dk = dk;
+  p.dv = dv;
   p.dwk = dwk;
   p.dwv = dwv;
+  p.dq_fp32 = dq_fp32 ? 1 : 0;
+  p.dkv_fp32 = dkv_fp32 ? 1 : 0;
   p.dw_fp32 = dw_fp32 ? 1 : 0;
   p.q_sb = q_sb; p.q_sh = q_sh; p.q_ss = q_ss;
   p.k_sb = k_sb; p.k_ss = k_ss; p.k_sh = k_sh;
@@ -734,14 +853,11 @@ extern "C" int dmla_bwd_onthefly(const void* q, const void* k, const void* v, co
   p.scale = softmax_scale;
   p.scale_log2 = softmax_scale * kLog2e;
   char* ws = static_cast<char*>(workspace);
-  p.q16 = reinterpret_cast<_Float16*>(ws + pl.off_q16);
-  p.do16 = reinterpret_cast<_Float16*>(ws + pl.off_do16);
   p.lse2 = reinterpret_cast<float*>(ws + pl.off_lse2);
   p.nd = reinterpret_cast<float*>(ws + pl.off_nd);
   p.klat = reinterpret_cast<_Float16*>(ws + pl.off_klat);
   p.vlat = reinterpret_cast<_Float16*>(ws + pl.off_vlat);
-  p.dklat = reinterpret_cast<_Float16*>(ws + pl.off_dklat);
-  p.dvlat = reinterpret_cast<_Float16*>(ws + pl.off_dvlat);
+  p.dxlat = reinterpret_cast<bf16*>(ws + pl.off_dx);
   p.wpart = reinterpret_cast<float*>(ws + pl.off_wpart);
   p.wt = reinterpret_cast<bf16*>(ws + pl.off_wt);
 

@@ -112,7 +112,8 @@ SIGNATURES = {
         [_ptr] * 14  # q, k, v, wk, wv, o, dout, m, l, dq, dk, dv, dwk, dwv
         + [_i64] * 6  # B, H, Sq, Sk, d_in, d_lat
         + [_i64] * 25  # q(3) k(3) v(3) w(2) o(3) dout(3) dq(3) dk(3) dw(2) strides
-        + [_int, _f32, _int, _ptr, _i64, _ptr],  # dw_fp32 scale causal ws ws_bytes stream
+        + [_int] * 3  # dq_fp32 dkv_fp32 dw_fp32
+        + [_f32, _int, _ptr, _i64, _ptr],  # scale causal ws ws_bytes stream
     ),
 }
 

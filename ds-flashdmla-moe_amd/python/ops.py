@@ -66,6 +66,20 @@ def _check_fp16_range(name: str, t: torch.Tensor) -> None:
              f"{name} has entries outside fp16's finite range (|x| <= 65504)")
 
 
+def _check_latent_range(name: str, x: torch.Tensor, w: torch.Tensor, mul: float) -> None:
+    """Raises unless the on-the-fly projection x[b, s, h, :] @ w[h] * mul stays inside fp16's
+    range for every row, by the bound max_s sum_i |x[.., s, h, i]| * max |w[h]| * mul: the dQ
+    kernel of the on-the-fly backward stores K_lat * scale * log2(e) and V_lat in fp16.  One
+    device sync."""
+    if x.numel() == 0:
+        return
+    row_l1 = x.float().abs().sum(dim=-1).amax(dim=(0, 1))          # [H]
+    w_max = w.float().abs().amax(dim=(1, 2))                        # [H]
+    bound = float((row_l1 * w_max).max()) * mul
+    _require(math.isfinite(bound) and bound <= 65504.0,
+             f"{name}'s projection may leave fp16's finite range (bound {bound:.4g} > 65504)")
+
+
 def _on_tensor_device(fn):
     """Runs an op with the device of its first GPU tensor argument current.  The library sizes
     its work and workspace, finds its static scratch and launches on the current device, so
@@ -443,15 +457,20 @@ def flash_dmla_bwd_onthefly(
     causal: bool = True,
     dw_dtype: torch.dtype = torch.float32,
     check_range: bool = False,
+    dq_dtype: Optional[torch.dtype] = None,
+    dkv_dtype: Optional[torch.dtype] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """On-the-fly DMLA backward from the saved statistics: returns (dq, dk, dv, dwk, dwv).
 
-    Shapes as for flash_dmla_fwd_onthefly; dq [B, H, Sq, 64], dk and dv [B, Sk, H, 128] in
-    bf16; dwk and dwv [H, 128, 64] in dw_dtype (default float32: they sum over every batch
-    element and position, and at config-4 sizes reach ~30, where a bf16 rounding alone is 0.06).
+    Shapes as for flash_dmla_fwd_onthefly; dq [B, H, Sq, 64] in dq_dtype (default q.dtype),
+    dk and dv [B, Sk, H, 128] in dkv_dtype (default k.dtype); dwk and dwv [H, 128, 64] in
+    dw_dtype (default float32: they sum over every batch element and position, and at config-4
+    sizes reach ~30, where a bf16 rounding alone is 0.06).  Each may be bfloat16 or float32.
     m, l must be the forward's statistics (return_stats=True).
-    Every product runs on fp16 operands with q, k, v, do and the weights converted exactly;
-    check_range=True verifies on the host (one device sync) that they stay inside fp16's range.
+    The dk / dv / weight side runs on bf16 operands, every rounded intermediate carried as a
+    bf16 pair hi + lo; dq runs on fp16 operands (q, do converted exactly, K_lat * scale *
+    log2(e) and V_lat rounded to fp16).  check_range=True verifies on the host (one device sync)
+    that q and do, and a bound of those projections, stay inside fp16's range.
     """
     _check_bf16("q", q, 4)
     _check_bf16("o", o, 4)
@@ -472,13 +491,19 @@ def flash_dmla_bwd_onthefly(
         _require(t.dtype == torch.float32 and t.is_cuda and t.is_contiguous() and tuple(t.shape) == (B, H, Sq),
                  f"{name} must be a contiguous float32 GPU tensor [B, H, Sq]")
     _same_device(q=q, k=k, v=v, wk=wk, wv=wv, o=o, do=do, m=m, l=l)
+    scale = _scale(softmax_scale, Dl)
     if check_range:
-        for name, t in (("q", q), ("k", k), ("v", v), ("do", do), ("wk", wk), ("wv", wv)):
+        for name, t in (("q", q), ("do", do)):
             _check_fp16_range(name, t)
-    dq = torch.empty((B, H, Sq, Dl), dtype=torch.bfloat16, device=q.device)
-    dk = torch.empty((B, Sk, H, Din), dtype=torch.bfloat16, device=q.device)
+        _check_latent_range("k", k, wk, scale / math.log(2.0))
+        _check_latent_range("v", v, wv, 1.0)
+    dq_dtype = q.dtype if dq_dtype is None else dq_dtype
+    dkv_dtype = k.dtype if dkv_dtype is None else dkv_dtype
+    _require(all(t in (torch.bfloat16, torch.float32) for t in (dq_dtype, dkv_dtype, dw_dtype)),
+             "gradient dtypes must be bfloat16 or float32")
+    dq = torch.empty((B, H, Sq, Dl), dtype=dq_dtype, device=q.device)
+    dk = torch.empty((B, Sk, H, Din), dtype=dkv_dtype, device=q.device)
     dv = torch.empty_like(dk)
-    _require(dw_dtype in (torch.bfloat16, torch.float32), "dw_dtype must be bfloat16 or float32")
     dwk = torch.empty((H, Din, Dl), dtype=dw_dtype, device=q.device)
     dwv = torch.empty_like(dwk)
     if B * H == 0:
@@ -496,8 +521,9 @@ def flash_dmla_bwd_onthefly(
         v.stride(0), v.stride(1), v.stride(2), wk.stride(0), wk.stride(1),
         o.stride(0), o.stride(1), o.stride(2), do.stride(0), do.stride(1), do.stride(2),
         dq.stride(0), dq.stride(1), dq.stride(2), dk.stride(0), dk.stride(1), dk.stride(2),
-        dwk.stride(0), dwk.stride(1), 1 if dw_dtype == torch.float32 else 0,
-        _scale(softmax_scale, Dl), 1 if causal else 0, _ptr(ws), ws_bytes, _stream(q),
+        dwk.stride(0), dwk.stride(1), 1 if dq_dtype == torch.float32 else 0,
+        1 if dkv_dtype == torch.float32 else 0, 1 if dw_dtype == torch.float32 else 0,
+        scale, 1 if causal else 0, _ptr(ws), ws_bytes, _stream(q),
     )
     return dq, dk, dv, dwk, dwv
 

@@ -273,8 +273,9 @@ int dmla_bwd_cache_latent(const void* q, const void* k_lat, const void* o, const
  *   q, k, v, wk, wv, o  as for dmla_fwd_onthefly (o is the forward's output)
  *   dout   [B, H, Sq, d_lat]  bf16  strides (do_sb, do_sh, do_ss)
  *   m, l   [B, H, Sq]         fp32  contiguous, exactly as dmla_fwd_onthefly wrote them
- *   dq     [B, H, Sq, d_lat]  bf16  strides (dq_sb, dq_sh, dq_ss)
- *   dk, dv [B, Sk, H, d_in]   bf16  strides (dk_sb, dk_ss, dk_sh), shared by both
+ *   dq     [B, H, Sq, d_lat]  bf16, or fp32 when dq_fp32 != 0; strides (dq_sb, dq_sh, dq_ss)
+ *   dk, dv [B, Sk, H, d_in]   bf16, or fp32 when dkv_fp32 != 0; strides (dk_sb, dk_ss, dk_sh),
+ *                             shared by both
  *   dwk, dwv [H, d_in, d_lat] bf16, or fp32 when dw_fp32 != 0; strides (dw_sh, dw_si, 1),
  *                             shared by both
  *
@@ -282,12 +283,14 @@ int dmla_bwd_cache_latent(const void* q, const void* k_lat, const void* o, const
  *   dS = P * (dP - D) with dP = dout V_lat^T:
  *     dq = scale dS K_lat,  dK_lat = scale dS^T q,  dV_lat = P^T dout,
  *     dk[b,:,h,:] = dK_lat[b,h] wk[h]^T,  dwk[h] = sum_b k[b,:,h,:]^T dK_lat[b,h]  (same for v).
- *   Rows with l = 0 contribute nothing.  Every product takes fp16 operands with fp32
- *   accumulation (inputs converted exactly for magnitudes in fp16's normal range; P, dS,
- *   dK_lat and dV_lat rounded to fp16).  Deterministic (no atomics).  workspace: device memory
- *   of at least dmla_bwd_onthefly_workspace_bytes(...) bytes, 16-byte aligned; its contents on
- *   entry do not matter.
- * Supported: d_in = 128, d_lat = 64, 0 < Sq, Sk <= 2^24.
+ *   Rows with l = 0 contribute nothing.  Products accumulate in fp32.  The dK_lat / dV_lat side
+ *   (and through it dk, dv, dwk, dwv) takes bf16 operands, every rounded one (K_lat, V_lat, P,
+ *   dS, dK_lat, dV_lat) as a bf16 pair hi + lo (within 2^-16 relative); dq takes fp16 operands
+ *   (q, dout converted exactly for magnitudes in fp16's normal range; K_lat, V_lat, dS rounded
+ *   to fp16).  Deterministic (no atomics).  workspace: device memory of at least
+ *   dmla_bwd_onthefly_workspace_bytes(...) bytes, 16-byte aligned; its contents on entry do not
+ *   matter.
+ * Supported: d_in = 128, d_lat = 64, 0 < Sq, Sk <= 2^24, row strides of q, dout, k, v below 2^24.
  */
 int64_t dmla_bwd_onthefly_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk,
                                           int64_t d_in, int64_t d_lat);
@@ -300,8 +303,8 @@ int dmla_bwd_onthefly(const void* q, const void* k, const void* v, const void* w
                       int64_t w_si, int64_t o_sb, int64_t o_sh, int64_t o_ss, int64_t do_sb,
                       int64_t do_sh, int64_t do_ss, int64_t dq_sb, int64_t dq_sh, int64_t dq_ss,
                       int64_t dk_sb, int64_t dk_ss, int64_t dk_sh, int64_t dw_sh, int64_t dw_si,
-                      int dw_fp32, float softmax_scale, int causal, void* workspace,
-                      int64_t workspace_bytes, dmla_stream_t stream);
+                      int dq_fp32, int dkv_fp32, int dw_fp32, float softmax_scale, int causal,
+                      void* workspace, int64_t workspace_bytes, dmla_stream_t stream);
 
 #ifdef __cplusplus
 }

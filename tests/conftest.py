@@ -50,33 +50,6 @@ def assert_out_close(out, ref, what="output"):
     return max_abs, mean_rel
 
 
-BF16_ROUNDING = 2.0 ** -8   # bf16's unit roundoff: 8-bit significand, half a step relative to 2^e
-
-
-def assert_out_close_scaled(out, ref, what="output", rel_max=0.0):
-    """The output bar with two widenings, each stated where it is used.  Every entry may differ
-    by OUT_MAX_ABS, plus rel_max * max|ref|, a normwise term for a path whose operands are
-    rounded relative to the whole tensor's scale.  A bf16 output may also differ by the bf16
-    rounding of its own reference entry (|ref| * 2^-8, which no bf16 value can beat; just
-    above 16 one rounding is up to 0.0625).  Mean-rel is checked as usual.
-    rel_max = 0 for every case held to the flat bar."""
-    bf16_out = out.dtype == torch.bfloat16
-    out = out.float()
-    ref = ref.float().to(out.device)
-    assert torch.isfinite(out).all(), f"{what}: non-finite values"
-    diff = (out - ref).abs()
-    allow = OUT_MAX_ABS + rel_max * ref.abs().max()
-    if bf16_out:
-        allow = allow + ref.abs() * BF16_ROUNDING
-    over = (diff - allow).max().item()
-    max_abs = diff.max().item()
-    mean_rel = (diff.mean() / ref.abs().mean().clamp_min(1e-30)).item()
-    assert over <= 0.0, (f"{what}: max-abs {max_abs:.3e} exceeds {OUT_MAX_ABS} + {rel_max:.2e} x max|ref|"
-                         f"{' + bf16 rounding' if bf16_out else ''} by {over:.3e}")
-    assert mean_rel <= OUT_MEAN_REL, f"{what}: mean-rel {mean_rel:.3e} > {OUT_MEAN_REL}"
-    return max_abs, mean_rel
-
-
 def assert_stats_close(m, l, m_ref, l_ref):
     m_ref = m_ref.float().to(m.device)
     l_ref = l_ref.float().to(l.device)

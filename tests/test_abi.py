@@ -180,8 +180,9 @@ def test_onthefly_bwd_workspace_query_and_argument_errors():
     P = ctypes.c_void_p
     need = lib.dmla_bwd_onthefly_workspace_bytes(2, 4, 100, 300, 128, 64)
     assert need > 0 and need % 256 == 0
-    # K_lat, V_lat, dK_lat, dV_lat as fp16 for every padded key, q and dO as fp16 per padded row
-    assert need >= 4 * 2 * 4 * 384 * 64 * 2 + 2 * 2 * 4 * 128 * 64 * 2
+    # per padded key: fp16 K_lat and V_lat, dK_lat and dV_lat as bf16 hi and lo planes; lse2
+    # and -D per padded row
+    assert need >= 6 * 2 * 4 * 384 * 64 * 2 + 2 * 2 * 4 * 128 * 4
     assert lib.dmla_bwd_onthefly_workspace_bytes(2, 4, 100, 300, 64, 64) == 0      # unsupported d_in
     assert lib.dmla_bwd_onthefly_workspace_bytes(0, 4, 100, 300, 128, 64) == 0     # empty problem
     assert lib.dmla_bwd_onthefly_workspace_bytes(1, 1, 1 << 25, 8, 128, 64) == 0   # above 2^24
@@ -196,7 +197,7 @@ def test_onthefly_bwd_workspace_query_and_argument_errors():
             *ptrs, a["B"], a["H"], a["Sq"], a["Sk"], a["din"], a["dlat"],
             2 * 64 * 64, 64 * 64, 64, 64 * a["ks"], a["ks"], 128, 64 * a["ks"], a["ks"], 128, 128 * 64, 64,
             2 * 64 * 64, 64 * 64, 64, 2 * 64 * 64, 64 * 64, 64, 2 * 64 * 64, 64 * 64, 64,
-            64 * 256, 256, 128, 128 * 64, 64, 1, a["scale"], 1, P(a["ws"]), max(ok - ws_short, 0), None)
+            64 * 256, 256, 128, 128 * 64, 64, 0, 0, 1, a["scale"], 1, P(a["ws"]), max(ok - ws_short, 0), None)
 
     assert call() == _lib.DMLA_ERR_WORKSPACE                         # 256 bytes short
     assert b"workspace" in lib.dmla_last_error()
@@ -207,6 +208,7 @@ def test_onthefly_bwd_workspace_query_and_argument_errors():
     assert call(scale=0.0) == _lib.DMLA_ERR_INVALID_ARG
     assert call(Sk=0) == _lib.DMLA_ERR_INVALID_ARG
     assert call(Sq=1 << 25) == _lib.DMLA_ERR_UNSUPPORTED
+    assert call(ks=1 << 24) == _lib.DMLA_ERR_UNSUPPORTED               # row stride past the copy offsets
     assert call(B=0, ws_short=0) == _lib.DMLA_OK                     # empty: nothing launched
     assert lib.dmla_last_error() == b""
 
@@ -218,6 +220,18 @@ def test_onthefly_bwd_python_wrapper_rejects_cpu_tensors():
     m = torch.zeros(1, 2, 4)
     with pytest.raises(ValueError, match="GPU tensor"):
         ops.flash_dmla_bwd_onthefly(q, k, k, w, w, q, q, m, m)
+
+
+def test_latent_range_check_bounds_the_projection():
+    # The on-the-fly backward's dQ kernel stores K_lat * scale * log2(e) and V_lat in fp16;
+    # check_range bounds them by max_s sum_i |x_i| * max |w| before any launch.
+    x = torch.ones(1, 3, 2, 128)
+    w = torch.full((2, 128, 64), 0.5)
+    ops._check_latent_range("k", x, w, 1.0)              # 128 * 0.5 = 64
+    w[1, 5, 7] = 600.0
+    with pytest.raises(ValueError, match="k's projection"):
+        ops._check_latent_range("k", x, w, 1.0)          # head 1: 128 * 600 > 65504
+    ops._check_latent_range("k", x, w, 0.5)              # scaled below the bound
 
 
 def test_fp16_range_check_rejects_values_the_kernels_would_saturate():
