@@ -80,9 +80,48 @@ def _settle(fn):
             return n
 
 
-def _time_launches(fn, steps, warmup):
+class _Roctx:
+    """ROCTx ranges around each workload's timed launches (libroctx64 through ctypes; a no-op
+    where the library is absent).  Under `rocprofv3 --marker-trace --kernel-trace` they let
+    --trace-summary average exactly the timed launches, not the settle and warm-up ones."""
+
+    _lib = None
+
+    @classmethod
+    def _load(cls):
+        if cls._lib is None:
+            import ctypes
+
+            cls._lib = False
+            for name in ("libroctx64.so", "libroctx64.so.4", "/opt/rocm/lib/libroctx64.so"):
+                try:
+                    lib = ctypes.CDLL(name)
+                except OSError:
+                    continue
+                lib.roctxRangePushA.argtypes = [ctypes.c_char_p]
+                lib.roctxRangePushA.restype = ctypes.c_int
+                lib.roctxRangePop.restype = ctypes.c_int
+                cls._lib = lib
+                break
+        return cls._lib
+
+    @classmethod
+    def push(cls, msg):
+        lib = cls._load()
+        if lib:
+            lib.roctxRangePushA(msg.encode())
+
+    @classmethod
+    def pop(cls):
+        lib = cls._load()
+        if lib:
+            lib.roctxRangePop()
+
+
+def _time_launches(fn, steps, warmup, tag=None):
     """Settles the clock (_settle), runs fn() warmup times, then `steps` timed times, then
     `steps` more with an event pair around each launch.  Returns (wall ms/step, kernel stats).
+    `tag` (workload, work per launch, unit) names the ROCTx range around the timed steps.
 
     The timed steps are bracketed by torch.cuda.synchronize() on both sides and by one HIP
     event pair on the launch stream (the current stream, which the C ABI receives), with
@@ -100,6 +139,8 @@ def _time_launches(fn, steps, warmup):
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    if tag is not None:
+        _Roctx.push("bench:%s:%d:%.6g:%s" % (tag[0], steps, tag[1], tag[2]))
     t0 = time.perf_counter()
     e0.record(stream)
     for i in range(steps):
@@ -107,6 +148,8 @@ def _time_launches(fn, steps, warmup):
     e1.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    if tag is not None:
+        _Roctx.pop()
     region_ms = e0.elapsed_time(e1) / steps
 
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
@@ -146,7 +189,7 @@ def bench_prefill(steps, warmup, cpu_baseline):
     def step(i=0):
         ops.flash_dmla_fwd(q, k, 512, SCALE, True)
 
-    wall_ms, ks = _time_launches(step, steps, warmup)
+    wall_ms, ks = _time_launches(step, steps, warmup, ("prefill", flops, "TFLOP/s"))
     res = {
         "metric": "DMLA prefill TFLOP/s (cache-latent fwd, config 2)",
         "value": flops / (wall_ms * 1e-3) / 1e12,
@@ -257,7 +300,7 @@ def bench_decode(steps, warmup, cpu_baseline):
         r = i % 3
         ops.flash_dmla_decode_paged(q, pools[r], tables[r], sl, 512, SCALE)
 
-    wall_ms, ks = _time_launches(step, steps, warmup)
+    wall_ms, ks = _time_launches(step, steps, warmup, ("decode", bytes_total, "GB/s"))
     res = {
         "metric": "DMLA paged decode KV GB/s (config 3)",
         "value": bytes_total / (wall_ms * 1e-3) / 1e9,
@@ -312,7 +355,7 @@ def bench_onthefly(steps, warmup, cpu_baseline):
     def step(i=0):
         ops.flash_dmla_fwd_onthefly(q, k, v, wk, wv, 0.125, True)
 
-    wall_ms, ks = _time_launches(step, steps, warmup)
+    wall_ms, ks = _time_launches(step, steps, warmup, ("onthefly", flops, "TFLOP/s"))
     res = {
         "metric": "DMLA on-the-fly prefill TFLOP/s (config 4)",
         "value": flops / (wall_ms * 1e-3) / 1e12,
@@ -359,7 +402,7 @@ def bench_bwd(steps, warmup, cpu_baseline):
     def step(i=0):
         ops.flash_dmla_bwd(q, k, o, do, m, l, 512, SCALE, True)
 
-    wall_ms, ks = _time_launches(step, steps, warmup)
+    wall_ms, ks = _time_launches(step, steps, warmup, ("bwd", flops, "TFLOP/s"))
     res = {
         "metric": "DMLA backward TFLOP/s (cache-latent, config 5)",
         "value": flops / (wall_ms * 1e-3) / 1e12,
@@ -414,7 +457,7 @@ def bench_onthefly_bwd(steps, warmup, cpu_baseline):
     def step(i=0):
         ops.flash_dmla_bwd_onthefly(q, k, v, wk, wv, o, do, m, l, 0.125, True)
 
-    wall_ms, ks = _time_launches(step, steps, warmup)
+    wall_ms, ks = _time_launches(step, steps, warmup, ("onthefly_bwd", flops, "TFLOP/s"))
     res = {
         "metric": "DMLA on-the-fly backward TFLOP/s (config-4 shapes)",
         "value": flops / (wall_ms * 1e-3) / 1e12,
@@ -464,6 +507,54 @@ def copy_calibration(mib):
     print(json.dumps({"copy_calibration_bytes": n, "launches": 5}))
 
 
+def _read_csv(path):
+    import csv
+
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def trace_summary(trace_dir):
+    """Per workload, the kernels rocprofv3 traced inside the ROCTx range around its timed launches
+    (`rocprofv3 --kernel-trace --marker-trace --output-format csv`): calls, mean / min / max
+    duration, their GPU time per step and the achieved rate that time gives.  Returns a list of
+    dicts, one per workload."""
+    import glob
+
+    def one(pattern):
+        hits = sorted(glob.glob(os.path.join(trace_dir, "**", pattern), recursive=True))
+        if not hits:
+            raise SystemExit(f"no {pattern} under {trace_dir}")
+        return _read_csv(hits[0])
+
+    kernels = one("*kernel_trace.csv")
+    markers = one("*marker_api_trace.csv")
+    ranges = []
+    for row in markers:
+        text = next((v for v in row.values() if isinstance(v, str) and v.startswith("bench:")), None)
+        if text is None:
+            continue
+        _, name, steps, work, unit = text.split(":", 4)
+        ranges.append((name, int(steps), float(work), unit, int(row["Start_Timestamp"]), int(row["End_Timestamp"])))
+    out = []
+    for name, steps, work, unit, t0, t1 in ranges:
+        per = {}
+        for k in kernels:
+            ks, ke = int(k["Start_Timestamp"]), int(k["End_Timestamp"])
+            if t0 <= ks and ke <= t1:
+                per.setdefault(k["Kernel_Name"], []).append((ke - ks) * 1e-3)   # us
+        total_us = sum(sum(v) for v in per.values())
+        gpu_ms = total_us * 1e-3 / steps
+        scale = 1e12 if unit == "TFLOP/s" else 1e9
+        peak = PEAK_BF16_TFLOPS if unit == "TFLOP/s" else PEAK_HBM_GBS
+        achieved = work / (gpu_ms * 1e-3) / scale if gpu_ms > 0 else None
+        out.append({"workload": name, "steps": steps, "kernel_ms_per_step": gpu_ms, "achieved": achieved,
+                    "unit": unit, "frac": achieved / peak if achieved else None,
+                    "kernels": {kn: {"calls": len(v), "mean_us": sum(v) / len(v), "min_us": min(v), "max_us": max(v)}
+                                for kn, v in sorted(per.items(), key=lambda kv: -sum(kv[1]))}})
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -475,7 +566,14 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget per workload")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run MIB-sized device copies (HBM counter calibration) and exit")
+    ap.add_argument("--trace-summary", metavar="DIR", default=None,
+                    help="summarise a rocprofv3 --kernel-trace --marker-trace CSV output directory of a bench run "
+                         "(the kernels inside each workload's timed range) and exit; needs no GPU")
     args = ap.parse_args()
+    if args.trace_summary:
+        for rec in trace_summary(args.trace_summary):
+            print(json.dumps(rec))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): every box here has a single GPU, "
               "so this build runs and reports the single-GPU path", file=sys.stderr)

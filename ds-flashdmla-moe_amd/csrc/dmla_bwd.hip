@@ -705,7 +705,9 @@ __global__ void __launch_bounds__(256) bwd_dk_reduce_kernel(BwdParams p) {
 constexpr int64_t kPairBytes = 8 * 4 * 256 * 2;
 
 // The cap on a chunk's dS' storage: DMLA_BWD_DS_CAP_BYTES, or the environment variable of that
-// name when set (tests use it to force several chunks at small sizes).
+// name when set (tests use it to force several chunks at small sizes).  Read once per plan: the
+// plan keeps it, and both the workspace sizing and the chunk loop of a call use that copy.
+// Like any environment variable it must not be changed while another thread calls in.
 int64_t ds_cap_bytes() {
   const char* e = getenv("DMLA_BWD_DS_CAP_BYTES");
   if (e != nullptr && *e) {
@@ -724,6 +726,7 @@ struct BwdChunk {
 struct BwdPlan {
   int R, n_rt, n_kb, n_pairs, kt_ld, n_groups;
   int n_chunks, max_pairs, max_items;
+  int64_t cap;     // dS' bytes per chunk, read once (ds_cap_bytes)
   int64_t off_lsed, off_kt, off_goff, off_ds, off_part, off_acc, bytes;
 };
 
@@ -762,9 +765,9 @@ BwdPlan make_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int causal, int 
   pl.n_pairs = (pl.n_kb + 1) / 2;
   pl.kt_ld = kKeys * pl.n_kb;
   pl.n_groups = (pl.n_rt + 3) / 4;
-  const int64_t cap = ds_cap_bytes();
+  pl.cap = ds_cap_bytes();
   for (int g0 = 0; g0 < pl.n_groups;) {
-    const BwdChunk c = next_chunk(pl, B, H, Sq, Sk, causal, cus, g0, cap);
+    const BwdChunk c = next_chunk(pl, B, H, Sq, Sk, causal, cus, g0, pl.cap);
     ++pl.n_chunks;
     pl.max_pairs = max(pl.max_pairs, c.pairs);
     pl.max_items = max(pl.max_items, c.n_items);
@@ -868,10 +871,10 @@ extern "C" int dmla_bwd_cache_latent(const void* q, const void* k_lat, const voi
   hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)pl.n_rt, (unsigned)B), dim3(256), 0, s, p);
   hipLaunchKernelGGL(bwd_kt_kernel, dim3(kDqk / 64, (unsigned)pl.n_kb, (unsigned)B), dim3(256), 0, s, p);
   const int cus = device_cu_count();
-  const int64_t cap = ds_cap_bytes();
   int chunk = 0;
   for (int g0 = 0; g0 < pl.n_groups; ++chunk) {
-    const BwdChunk c = next_chunk(pl, B, H, Sq, Sk, causal ? 1 : 0, cus, g0, cap);
+    // the plan's own cap: the chunks are the ones its workspace regions were sized for
+    const BwdChunk c = next_chunk(pl, B, H, Sq, Sk, causal ? 1 : 0, cus, g0, pl.cap);
     p.rt_begin = 4 * c.g0;
     p.rt_end = min(pl.n_rt, 4 * c.g1);
     p.chunk_pairs = c.pairs;
