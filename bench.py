@@ -93,7 +93,9 @@ class _Roctx:
             import ctypes
 
             cls._lib = False
-            for name in ("libroctx64.so", "libroctx64.so.4", "/opt/rocm/lib/libroctx64.so"):
+            # rocprofv3 traces the ROCTx of rocprofiler-sdk; the older libroctx64 is the fallback
+            for name in ("librocprofiler-sdk-roctx.so", "/opt/rocm/lib/librocprofiler-sdk-roctx.so",
+                         "libroctx64.so", "/opt/rocm/lib/libroctx64.so"):
                 try:
                     lib = ctypes.CDLL(name)
                 except OSError:

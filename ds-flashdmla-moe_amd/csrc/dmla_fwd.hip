@@ -134,7 +134,7 @@ struct Work {
 // first_range[B], range_start[R + 1] (first tile of each range, in the concatenated tile
 // space), range_first_b[R] (the sequence holding the range's first tile).
 constexpr int kPlanHeader = 8;
-constexpr int kSegCost = 16;                          // measured ~10 us per segment, ~1.04 us per tile; 8-16 time alike
+constexpr int kSegCost = 10;   // per-segment cost in tiles: a launch timeline fits 0.92 us per tile + 9.2 us per segment
 constexpr int kMaxSegTiles = 2 * kMaxSegPages - 2;   // a segment's pages fit its page registers
 __host__ __device__ inline int64_t plan_ints(int64_t B, int64_t R) { return kPlanHeader + 4 * B + 2 + 2 * R + 1; }
 // Inline plan: the decode kernel builds the plan itself, in LDS past the pipeline's area, when

@@ -187,7 +187,7 @@ def dmla_decode_paged(q: Tensor, kv_pool: Tensor, block_table: Tensor, cache_seq
 
 
 def decode_plan(cache_seqlens, n_ranges: int, max_pages: int, page_size: int = 64, tile: int = 32,
-                seg_cost: int = 16):
+                seg_cost: int = 10):
     """The decode tile-scheduler plan for R = n_ranges (no reference counterpart).
 
     The 32-token tiles of all sequences, in order, are cut into R ranges that are equal in a
@@ -238,7 +238,7 @@ def decode_plan(cache_seqlens, n_ranges: int, max_pages: int, page_size: int = 6
 
 
 def decode_ranges(B: int, H: int, max_pages: int, cu_count: int, page_size: int = 64, tile: int = 32,
-                  seg_cost: int = 16, max_seg_pages: int = 128) -> int:
+                  seg_cost: int = 10, max_seg_pages: int = 128) -> int:
     """Range count R of a decode plan (no reference counterpart): one range per CU and group of
     64 heads (a multiple of 8 from 8 on), raised so that a range spans at most
     2*max_seg_pages - 2 tiles when every sequence is full."""

@@ -377,7 +377,7 @@ def test_decode_plan_covers_every_tile_once(lens, nr):
     plan = R.decode_plan(lens, nr, 128)
     hdr, tp, sb, ns, rs, seen, splits, segs = _walk_plan(plan, lens)
     B = len(lens)
-    assert hdr[0] == B and hdr[1] == nr and hdr[5] == 16
+    assert hdr[0] == B and hdr[1] == nr and hdr[5] == 10
     total = sum((x + 31) // 32 for x in lens)
     assert hdr[3] == total and len(seen) == total and rs[0] == 0 and rs[-1] == total
     assert all(rs[i] <= rs[i + 1] for i in range(nr))
@@ -390,10 +390,11 @@ def test_decode_plan_balances_tiles_plus_segment_costs():
     lens = torch.randint(1024, 8193, (64,), generator=g).tolist()
     plan = R.decode_plan(lens, 128, 128)
     hdr, tp, sb, ns, rs, seen, splits, segs = _walk_plan(plan, lens)
-    W = hdr[2]
-    cost = [(rs[r + 1] - rs[r]) + 16 * segs[r] for r in range(128)]
+    W, c = hdr[2], hdr[5]
+    assert c == 10
+    cost = [(rs[r + 1] - rs[r]) + c * segs[r] for r in range(128)]
     # every range's weighted cost is within one segment cost of W (the first segment included)
-    assert max(cost) <= W + 16 and min(c for c in cost if c) >= W - 16 - 16
+    assert max(cost) <= W + c and min(x for x in cost if x) >= W - 2 * c
 
 
 @pytest.mark.parametrize("cus", [256, 304, 80])
