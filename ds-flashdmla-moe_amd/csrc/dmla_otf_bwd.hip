@@ -9,11 +9,11 @@
 //     dK = dK_lat WK^T,  dWK[h] = sum_{b,s} K[b,s,h,:]^T dK_lat[b,h,s,:]   (same for V / WV).
 // The reference has no on-the-fly backward at all (WK / WV are learnable per README.md:14).
 //
-// Seven kernels run in order on one stream, all deterministic (no atomics):
+// Six kernels run in order on one stream, all deterministic (no atomics):
 //   otf_bwd_prep_kernel    per query row: lse2 = (m + ln l) log2(e) and -D;
 //   otf_bwd_wt_kernel      WK^T and WV^T;
-//   otf_bwd_proj_kernel    K_lat and V_lat as fp16, for the dQ kernel;
-//   otf_bwd_dkdv_kernel    per 128 keys: dK_lat, dV_lat over the rows that see them;
+//   otf_bwd_dkdv_kernel    per 128 keys: projects their K_lat and V_lat (also stored in fp16
+//                          for the dQ kernel), then dK_lat, dV_lat over the rows that see them;
 //   otf_bwd_dq_kernel      per 128 rows: dQ over the keys they see (S and dP recomputed);
 //   otf_bwd_wgrad_kernel   per (tensor, head, 1024 keys): dK / dV and a dWK / dWV partial;
 //   otf_bwd_wreduce_kernel sums the partials of each head in a fixed order.
@@ -194,59 +194,6 @@ __global__ void __launch_bounds__(256) otf_bwd_wt_kernel(OtfBwdParams p) {
   }
 }
 
-// Projection for the dQ kernel, rounded to fp16: X_lat^T = W^T X^T with A = W^T rows and
-// B = raw X rows, four k-steps of 32 input dims each.  Block = 256 keys of one (b, h); waves
-// 0-1 project K, waves 2-3 V, each taking every other 16-key block with the next block's rows
-// loaded while the current one is multiplied.  Grid (H, Skp / 256 rounded up, B).
-__global__ void __launch_bounds__(256) otf_bwd_proj_kernel(OtfBwdParams p) {
-  // Heads fastest in the grid: workgroups issued together read neighbouring 256-byte pieces of
-  // the same [B, S, H, 128] rows (the 16 key blocks of one head lie 8 KB apart per key).
-  const int h = blockIdx.x, b = blockIdx.z, bh = b * p.H + h;
-  const int wave = uniform(threadIdx.x >> 6), lane = lane_id(), l16 = lane & 15, g = lane >> 4;
-  const int x = wave >> 1;
-  bf16x8 wa[4][4];   // [db][ks]: W^T row 16 db + l16, input dims 32 ks + 8 g ..
-  {
-    const bf16* wt = p.wt + ((size_t)x * p.H + h) * (kLat * kIn) + l16 * kIn + 8 * g;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) wa[db][ks] = *reinterpret_cast<const bf16x8*>(wt + 16 * db * kIn + 32 * ks);
-  }
-  const bf16* src = x ? p.v + b * p.v_sb + h * p.v_sh : p.k + b * p.k_sb + h * p.k_sh;
-  const int64_t ss = x ? p.v_ss : p.k_ss;
-  _Float16* dst = (x ? p.vlat : p.klat) + (size_t)bh * p.Skp * kLat;
-  const int key_base = blockIdx.y * 256;
-  const int n_kb = min(16, (p.Skp - key_base) / 16);
-  bf16x8 xr[4];
-  auto load = [&](int kb) {
-    const int gk = min(key_base + 16 * kb + l16, p.Sk - 1);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) xr[ks] = *reinterpret_cast<const bf16x8*>(src + (int64_t)gk * ss + 32 * ks + 8 * g);
-  };
-  int kb = wave & 1;
-  if (kb < n_kb) load(kb);
-  for (; kb < n_kb; kb += 2) {
-    bf16x8 cur[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) cur[ks] = xr[ks];
-    if (kb + 2 < n_kb) load(kb + 2);
-    const int key = key_base + 16 * kb + l16;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      f32x4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) c = mfma_bf16(wa[db][ks], cur[ks], c);   // X_lat^T[dim 16 db + 4 g + i][key]
-      f16x4 o;
-      // K_lat is stored multiplied by scale log2(e): S then comes out in log2 units and the
-      // score accumulators can start at -lse2 (dQ takes ln 2 instead of the scale).
-      const float mul = x ? 1.f : p.scale_log2;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = key < p.Sk ? (_Float16)(c[i] * mul) : (_Float16)0.f;
-      *reinterpret_cast<f16x4*>(dst + (size_t)key * kLat + 16 * db + 4 * g) = o;
-    }
-  }
-}
-
 // X_lat * mul of keys k0 + 16 kb + l16 (kb = 0, 1) as bf16 pairs (hi, lo), each in the layout
 // of an MFMA B operand whose k index runs over dims 32 ks + 8 g .. +7 (lane l, g = l/16).
 // Projected here from the raw rows: X_lat^T = W^T X^T over four k-steps of 32 input dims.  A C
@@ -282,6 +229,7 @@ __device__ __forceinline__ void project_keys(const OtfBwdParams& p, int x, int b
       }
     }
   const float mul = x ? 1.f : p.scale_log2;
+  _Float16* dst16 = (x ? p.vlat : p.klat) + ((size_t)(b * p.H + h) * p.Skp + k0 + l16) * kLat + 8 * g;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     const bool live = k0 + 16 * kb + l16 < p.Sk;
@@ -289,6 +237,7 @@ __device__ __forceinline__ void project_keys(const OtfBwdParams& p, int x, int b
     for (int ks = 0; ks < 2; ++ks) {
       float v[8];
       __bf16 vh[8], vl[8];
+      f16x8 v16;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         v[i] = live ? c[ks][0][kb][i] * mul : 0.f;
@@ -299,7 +248,10 @@ __device__ __forceinline__ void project_keys(const OtfBwdParams& p, int x, int b
       for (int j = 0; j < 8; ++j) {
         hi[kb][ks][j] = vh[j];
         lo[kb][ks][j] = vl[j];
+        v16[j] = (_Float16)v[j];
       }
+      // the fp16 copy the dQ kernel stages: row key, dims 32 ks + 8 g .. +7
+      *reinterpret_cast<f16x8*>(dst16 + 16 * kb * kLat + 32 * ks) = v16;
     }
   }
 }
@@ -817,7 +769,7 @@ extern "C" int dmla_bwd_onthefly(const void* q, const void* k, const void* v, co
                 (long long)pl.bytes, (long long)workspace_bytes);
   if (!aligned16(workspace)) return fail(DMLA_ERR_INVALID_ARG, "dmla_bwd_onthefly: workspace must be 16-byte aligned");
   const int64_t grid_kv = B * H * (pl.Skp / kKeyBlk), grid_q = B * H * (pl.Sqp / kRowBlk);
-  if (grid_kv > 0x7fffffff || grid_q > 0x7fffffff || B * H > 65535 || 2 * B > 65535 || (pl.Skp + 255) / 256 > 65535)
+  if (grid_kv > 0x7fffffff || grid_q > 0x7fffffff || B * H > 65535 || 2 * B > 65535)
     return fail(DMLA_ERR_UNSUPPORTED, "dmla_bwd_onthefly: grid too large");
 
   OtfBwdParams p = {};
@@ -864,8 +816,6 @@ extern "C" int dmla_bwd_onthefly(const void* q, const void* k, const void* v, co
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(otf_bwd_prep_kernel, dim3((unsigned)(pl.Sqp / 32), (unsigned)(B * H)), dim3(256), 0, s, p);
   hipLaunchKernelGGL(otf_bwd_wt_kernel, dim3((unsigned)H, 2), dim3(256), 0, s, p);
-  hipLaunchKernelGGL(otf_bwd_proj_kernel, dim3((unsigned)H, (unsigned)((pl.Skp + 255) / 256), (unsigned)B), dim3(256),
-                     0, s, p);
   hipLaunchKernelGGL(otf_bwd_dkdv_kernel, dim3((unsigned)grid_kv), dim3(256), 0, s, p);
   hipLaunchKernelGGL(otf_bwd_dq_kernel, dim3((unsigned)grid_q), dim3(256), 0, s, p);
   hipLaunchKernelGGL(otf_bwd_wgrad_kernel, dim3((unsigned)pl.n_sc, (unsigned)H, (unsigned)(2 * B)), dim3(256), 0, s, p);
