@@ -94,6 +94,7 @@ struct BwdParams {
   _Float16* kt;         // [B][576][kt_ld] fp16
   int32_t* goff;        // [n_groups + 1]: first (group, key block) pair of each group
   _Float16* ds;         // [B][chunk_pairs][8 row blocks][4 key blocks][256]: fp16 dS' 16x16 blocks, MFMA C order
+                        // with lane c's 4 values at slot ds_slot(c)
   float* part;          // [n_items][2][4 kb][36 cb][64 lanes][4]: dK_lat partials in MFMA C order
   float* dk_acc;        // fp32 dK_lat of the chunks so far: [B][Sk][576], or the fp32 output itself
 };
@@ -138,6 +139,12 @@ __host__ __device__ inline PairPlan pair_plan(int causal, int Sq, int Sk, int H,
 __host__ __device__ inline int part_begin(int total, int parts, int j) {
   return (int)(((int64_t)total * j) / parts);
 }
+
+// Slot of C-order lane c in a stored 16x16 dS' block (8 bytes per slot): bit 2 of the lane
+// index flipped for lanes 32-63.  The dQ kernel's transposed reads of a block then take 32
+// distinct slots modulo 32 (the 64 LDS banks) per 32 lanes; plain C order put lanes q and q + 2
+// of a read on the same banks (a 2-way conflict on every dS' read).
+__host__ __device__ inline int ds_slot(int c) { return c ^ ((c >> 3) & 4); }
 
 __device__ __forceinline__ f16x4 to_f16x4(float a, float b, float c, float d) {
   f16x4 r;
@@ -475,7 +482,7 @@ bwd_dkdv_kernel(BwdParams p) {
         *reinterpret_cast<DMLA_LDS f16x4*>(xbuf + kbl * 1024 + lane * 16 + 8 * rb) = pb;
         *reinterpret_cast<DMLA_LDS f16x4*>(xbuf + 4096 + kbl * 1024 + lane * 16 + 8 * rb) = db;
         _Float16* dsblk = p.ds + ((ds_pair * 8 + 2 * (rt & 3) + rb) * 4 + kbl) * 256;
-        *reinterpret_cast<f16x4*>(dsblk + 4 * lane) = db;
+        *reinterpret_cast<f16x4*>(dsblk + 4 * ds_slot(lane)) = db;
       }
       __syncthreads();   // exchange written
       if (more) row_stats(rt + dir);
@@ -588,8 +595,11 @@ __global__ void __launch_bounds__(kDqThreads, 1) bwd_dq_kernel(BwdParams p) {
     for (int m = 0; m < 6; ++m) copy(kt, st, m);
   };
   // dS' A operand of row block rq, half h: lane 4e+q of group g reads C-order lane
-  // 16 q + 8 (g & 1) + 4 h + e of key block g >> 1 (see the tr-read rule in dmla_common.h).
-  const int a_off = 4 * rh * 1024 + (g >> 1) * 512 + 8 * (16 * qq + 8 * (g & 1) + e);
+  // 16 q + 8 (g & 1) + 4 h + e of key block g >> 1 (see the tr-read rule in dmla_common.h), at
+  // its stored slot ds_slot().
+  const int a_c = 16 * qq + 8 * (g & 1) + e;
+  const int a_off0 = 4 * rh * 1024 + (g >> 1) * 512 + 8 * ds_slot(a_c);
+  const int a_off1 = 4 * rh * 1024 + (g >> 1) * 512 + 8 * ds_slot(a_c + 4);
   // K^T B operand of column block wc + 4u: dim row 16 cb + l16, logical chunk g.
   const int b_off = kDqDsBytes + wc * 1024 + l16 * 64 + 16 * (g ^ e);
 
@@ -613,9 +623,9 @@ __global__ void __launch_bounds__(kDqThreads, 1) bwd_dq_kernel(BwdParams p) {
     f16x8 a[4];
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq) {
-      const DMLA_LDS char* ab = sb + rq * 1024 + a_off;
-      const f16x4 lo = lds_read_tr16_f16(reinterpret_cast<const DMLA_LDS f16x4*>(ab));
-      const f16x4 hi = lds_read_tr16_f16(reinterpret_cast<const DMLA_LDS f16x4*>(ab + 32));
+      const DMLA_LDS char* ab = sb + rq * 1024;
+      const f16x4 lo = lds_read_tr16_f16(reinterpret_cast<const DMLA_LDS f16x4*>(ab + a_off0));
+      const f16x4 hi = lds_read_tr16_f16(reinterpret_cast<const DMLA_LDS f16x4*>(ab + a_off1));
       a[rq] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     }
 #pragma unroll
