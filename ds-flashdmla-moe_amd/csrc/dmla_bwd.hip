@@ -356,11 +356,14 @@ bwd_dkdv_kernel(BwdParams p) {
       for (int v = 0; v < 9; ++v) acc[a][v] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // Staging of row tile rt into LDS stage st (rows past R re-read row R-1: finite, and masked
-    // by their +inf lse2): this lane's row sources, then 17 copies (9 Q chunk groups, 8 dO
-    // groups) issued one per S-phase step and one per early dK-phase operand, so the CU's
-    // vector-memory path (about 64 B per clock: ~1000 clocks for the 68 KB tile) works under the
-    // MFMAs instead of stalling the wave in one burst, and the last copy still has the second
-    // half of the dK-phase to land.
+    // by their +inf lse2): this lane's row sources, then 17 copies: the 9 Q chunk groups one per
+    // S-phase step, the 8 dO groups two per step in the first four dK-phase steps.  The CU's
+    // vector-memory path moves about 64 B per clock (~1000 clocks for the 68 KB tile), so the
+    // copies are spread under the MFMAs instead of stalling the wave in one burst.  Measured
+    // alternatives (kernel-trace A/B at config 5): all 17 in the S-phase stalled it by ~1000
+    // clocks per tile; the dO copies one per step over the first eight dK steps left the next
+    // tile's barrier ~1000 clocks of wait (2 % slower); issued around the partial swap or with
+    // the dS' stores, they slowed every phase after them (8 % slower).
     const char* qsrc = nullptr;
     const char* osrc = nullptr;
     unsigned cdst = 0;
@@ -493,41 +496,51 @@ bwd_dkdv_kernel(BwdParams p) {
       for (int kbl = 0; kbl < 4; ++kbl) {
         pT[kbl] = *reinterpret_cast<const DMLA_LDS f16x8*>(xbuf + kbl * 1024 + lane * 16);
         dsT[kbl] = *reinterpret_cast<const DMLA_LDS f16x8*>(xbuf + 4096 + kbl * 1024 + lane * 16);
-        asm volatile("" : "+a"(pT[kbl]));   // A operands of the whole phase: AGPR file
-        asm volatile("" : "+a"(dsT[kbl]));
       }
+      // A operands of the whole phase: AGPR file.  One statement for all eight, so the reads go
+      // out together and are awaited once (one statement per operand had the compiler issue
+      // them two at a time, each pair awaited before the next).
+      asm volatile("" : "+a"(pT[0]), "+a"(pT[1]), "+a"(pT[2]), "+a"(pT[3]), "+a"(dsT[0]), "+a"(dsT[1]),
+                   "+a"(dsT[2]), "+a"(dsT[3]));
       // Column operands of column block wave + 4v (v < 9: Q; v >= 9: dO block v - 9), as two
-      // transposed half reads each; read in batches of 3 operands ahead of their MFMAs.
+      // transposed half reads each.  Software pipeline over the 17 operands: step v issues the
+      // reads of operand v + 3, the 4 MFMAs of operand v and, between them, the fp16
+      // conversion of operand v + 1, so each read has two steps (8 MFMAs) to land.  The
+      // schedule is pinned with scheduling-group barriers: left to itself the compiler issued
+      // each operand's reads right before its conversion and waited for them there, one LDS
+      // round trip per operand.
       auto k_read = [&](int v, bf16x4& lo, bf16x4& hi) {
         const DMLA_LDS char* c = v < 9 ? qt + v * kGroupBytes + b_off : ot + (v - 9) * kGroupBytes + b_off;
         lo = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(c));
         hi = lds_read_tr16(reinterpret_cast<const DMLA_LDS bf16x4*>(c + 16 * 128));
       };
-      bf16x4 kl[2][3], kh[2][3];
+      bf16x4 kl[4], kh[4];   // raw operands, ring slot v & 3
 #pragma unroll
-      for (int j = 0; j < 3; ++j) k_read(j, kl[0][j], kh[0][j]);
+      for (int j = 0; j < 3; ++j) k_read(j, kl[j], kh[j]);
+      f16x8 bnext = bf16_to_f16(kl[0], kh[0]);
 #pragma unroll
-      for (int bt = 0; bt < 6; ++bt) {   // operands 0..16 in batches of 3 (the last holds 2)
-        if (bt + 1 < 6) {
-#pragma unroll
-          for (int j = 0; j < 3; ++j)
-            if (3 * (bt + 1) + j < 17) k_read(3 * (bt + 1) + j, kl[(bt + 1) & 1][j], kh[(bt + 1) & 1][j]);
+      for (int v = 0; v < 17; ++v) {
+        if (v + 3 < 17) k_read(v + 3, kl[(v + 3) & 3], kh[(v + 3) & 3]);
+        if (v < kOGroups / 2) {   // the next tile's dO chunk groups 2v, 2v + 1
+          stage_copy(kQGroups + 2 * v);
+          stage_copy(kQGroups + 2 * v + 1);
         }
+        const f16x8 bop = bnext;
+        if (v + 1 < 17) bnext = bf16_to_f16(kl[(v + 1) & 3], kh[(v + 1) & 3]);
+        if (v < 9) {
 #pragma unroll
-        for (int j = 0; j < 3; ++j) {
-          const int v = 3 * bt + j;
-          if (v < 17) {
-            if (v < kOGroups) stage_copy(kQGroups + v);   // the next tile's dO chunk group v
-            const f16x8 bop = bf16_to_f16(kl[bt & 1][j], kh[bt & 1][j]);
-            if (v < 9) {
+          for (int kbl = 0; kbl < 4; ++kbl) acc[kbl][v] = mfma_f16(dsT[kbl], bop, acc[kbl][v]);
+        } else {
 #pragma unroll
-              for (int kbl = 0; kbl < 4; ++kbl) acc[kbl][v] = mfma_f16(dsT[kbl], bop, acc[kbl][v]);
-            } else {
-#pragma unroll
-              for (int kbl = 0; kbl < 4; ++kbl) acc[kbl][v - 9] = mfma_f16(pT[kbl], bop, acc[kbl][v - 9]);
-            }
-          }
+          for (int kbl = 0; kbl < 4; ++kbl) acc[kbl][v - 9] = mfma_f16(pT[kbl], bop, acc[kbl][v - 9]);
         }
+        if (v + 3 < 17) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // reads of operand v + 3
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // an MFMA of operand v
+          if (v + 1 < 17) __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // a quarter of the conversion
+        }
+        __builtin_amdgcn_sched_barrier(0);   // nothing crosses a step boundary
       }
     }
 
