@@ -162,15 +162,33 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
       constexpr bool kK = decltype(is_k)::value;
       const DMLA_LDS char* raw = lds + kRawOff + (st * 2 + (kK ? 0 : 1)) * kRawBytes;
       DMLA_LDS char* lat = lds + kLatOff + (lb * 2 + (kK ? 0 : 1)) * kLatBytes;
+      // The four key blocks' accumulations run interleaved (k-step outer), so consecutive MFMAs
+      // are independent, and each k-step's raw reads go out one k-step ahead.  (Key block by key
+      // block, every MFMA waited for the previous one's result and every read was awaited
+      // right before its MFMA.)
+      f32x4 cacc[4];
+      bf16x8 xr[2][4];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
-        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+        cacc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        xr[0][kb] = *reinterpret_cast<const DMLA_LDS bf16x8*>(raw + raw_off(16 * kb + l16, g));
+      }
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 x = *reinterpret_cast<const DMLA_LDS bf16x8*>(raw + raw_off(16 * kb + l16, 4 * ks + g));
-          if constexpr (kK) c = mfma_bf16(wreg[ks], x, c);   // K_lat^T[dim 16 pdb + 4g + i][key 16 kb + l16]
-          else c = mfma_bf16(x, wreg[ks], c);                // V_lat[key 16 kb + 4g + i][dim 16 pdb + l16]
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks + 1 < 4) {
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb)
+            xr[(ks + 1) & 1][kb] = *reinterpret_cast<const DMLA_LDS bf16x8*>(raw + raw_off(16 * kb + l16, 4 * (ks + 1) + g));
         }
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          if constexpr (kK) cacc[kb] = mfma_bf16(wreg[ks], xr[ks & 1][kb], cacc[kb]);   // K_lat^T[dim 16 pdb + 4g + i][key 16 kb + l16]
+          else cacc[kb] = mfma_bf16(xr[ks & 1][kb], wreg[ks], cacc[kb]);                // V_lat[key 16 kb + 4g + i][dim 16 pdb + l16]
+        }
+      }
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        f32x4 c = cacc[kb];
         if constexpr (kK) {
           // K_lat is stored pre-multiplied by scale log2(e), so that scores come out of the MFMA
           // in log2 units, as hi + lo with hi = bf16(c) and lo = bf16(c - hi):
