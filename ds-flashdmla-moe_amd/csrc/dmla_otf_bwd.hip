@@ -474,6 +474,12 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
 
   auto subtile = [&](const DMLA_LDS char* kt, const DMLA_LDS char* vt, int c0, auto mask_tag) {
     constexpr bool kMask = decltype(mask_tag)::value;
+    // The dQ product's K_lat column operands do not depend on S or dP: their reads go out first
+    // (kept there by the scheduling barrier), so they have landed by the time dS is formed.
+    f16x8 kcol[4];   // K_lat[keys][dim 16 db + l16]
+#pragma unroll
+    for (int db = 0; db < 4; ++db) kcol[db] = lds_col_operand(kt, lane, db);
+    __builtin_amdgcn_sched_barrier(0);
     f32x4 sT[2][2], dpT[2][2];   // [kb][rb]: keys 16 kb + 4 g + i, row 16 rb + l16
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -505,11 +511,9 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
           dsa[rb][4 * kb + i] = (_Float16)(pv * dpT[kb][rb][i]);
         }
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      const f16x8 kb_t = lds_col_operand(kt, lane, db);   // K_lat[keys][dim 16 db + l16]
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) dq[rb][db] = mfma_f16(dsa[rb], kb_t, dq[rb][db]);
-    }
+      for (int rb = 0; rb < 2; ++rb) dq[rb][db] = mfma_f16(dsa[rb], kcol[db], dq[rb][db]);
   };
 
   // Unrolled by two stages so that the buffer offset is an instruction immediate.
