@@ -332,6 +332,13 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
         dpacc[rb][kb] = mfma_bf16(oa1, vhi[kb][1], d);
       }
     }
+    // Column operands of the dV / dK updates (dO^T, Q^T of dims 16 db ..), one step ahead: those
+    // of db = 0 go out before the exp2 work (held there by the scheduling barrier), those of
+    // db + 1 while the MFMAs of db run.  (Read right before their MFMAs, each group's LDS round
+    // trip was waited out.)
+    bf16x8 otn = lds_col_operand_bf(dt, lane, 0);
+    bf16x8 qtn = lds_col_operand_bf(qt, lane, 0);
+    __builtin_amdgcn_sched_barrier(0);
     bf16x8 pbh[2], pbl[2], dsh[2], dsl[2];   // [kb]: B operands, slot 4 rb + i = row 16 rb + 4 g + i
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -354,8 +361,12 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
     }
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const bf16x8 ot = lds_col_operand_bf(dt, lane, db);   // dO^T[dim 16 db + l16][rows]
-      const bf16x8 qtt = lds_col_operand_bf(qt, lane, db);  // Q^T
+      const bf16x8 ot = otn;    // dO^T[dim 16 db + l16][rows]
+      const bf16x8 qtt = qtn;   // Q^T
+      if (db + 1 < 4) {
+        otn = lds_col_operand_bf(dt, lane, db + 1);
+        qtn = lds_col_operand_bf(qt, lane, db + 1);
+      }
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         dvt[db][kb] = mfma_bf16(ot, pbl[kb], dvt[db][kb]);
@@ -363,6 +374,9 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
         dkt[db][kb] = mfma_bf16(qtt, dsl[kb], dkt[db][kb]);
         dkt[db][kb] = mfma_bf16(qtt, dsh[kb], dkt[db][kb]);
       }
+      if (db + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // reads of db + 1
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);                   // MFMAs of db
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
