@@ -148,6 +148,7 @@ struct InlinePlan {
   int ns[kInlinePlanB];        // split count
   int fr[kInlinePlanB];        // first range
   int sb[kInlinePlanB + 1];    // first partial slot
+  int ctx[kInlinePlanB];       // context length, clamped to the block table
   int rs[kInlinePlanR + 1];    // range starts
   int tmp[kWaves];             // scan scratch
 };
@@ -794,7 +795,11 @@ __device__ __forceinline__ void build_inline_plan(const MqaParams& p, DMLA_LDS I
   const int tid = threadIdx.x;
   const int B = p.B, R = p.n_ranges;
   int nt = 0;
-  if (tid < B) nt = (min(max(p.seqlens[tid], 0), p.max_pages * kPage) + kTileN - 1) / kTileN;
+  int ctx = 0;
+  if (tid < B) {
+    ctx = min(max(p.seqlens[tid], 0), p.max_pages * kPage);
+    nt = (ctx + kTileN - 1) / kTileN;
+  }
   int total, nonempty;
   const int tpb = wg_exclusive_scan(nt, ip->tmp, total);
   const int nb = wg_exclusive_scan(nt > 0 ? 1 : 0, ip->tmp, nonempty);
@@ -832,6 +837,7 @@ __device__ __forceinline__ void build_inline_plan(const MqaParams& p, DMLA_LDS I
   const int sbb = wg_exclusive_scan(ns, ip->tmp, nsplits);
   if (tid < B) {
     ip->ns[tid] = ns;
+    ip->ctx[tid] = ctx;
     ip->fr[tid] = fr;
     ip->sb[tid] = sbb;
   }
@@ -917,7 +923,9 @@ __global__ __launch_bounds__(kThreads, 1) void mqa_fwd_kernel(MqaParams p) {
       if (seg0 >= seg1) continue;   // an empty sequence (its output comes from the combine)
       wk.b = bseq;
       wk.row0 = k * kRowsPerWG;
-      wk.ctx = min(max(p.seqlens[bseq], 0), p.max_pages * kPage);
+      // From the inline plan when there is one: a global load here would also wait for the
+      // previous segment's output stores (loads and stores share one counter).
+      wk.ctx = inl ? ip->ctx[bseq] : min(max(p.seqlens[bseq], 0), p.max_pages * kPage);
       wk.tile_begin = seg0 - tb;
       wk.tile_end = seg1 - tb;
       wk.page_begin = wk.tile_begin / (kPage / kTileN);
