@@ -336,18 +336,29 @@ bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
     for (int kbl = 0; kbl < 4; ++kbl) {
       const int key = key0 + 16 * kbl + l16;
-      const bool kvalid = key < p.Sk;
-      const bf16* krow = p.k + b * p.k_sb + (int64_t)(kvalid ? key : 0) * p.k_ss + 8 * g;
+      const bf16* krow = p.k + b * p.k_sb + (int64_t)(key < p.Sk ? key : 0) * p.k_ss + 8 * g;
 #pragma unroll
       for (int j = 0; j < 9; ++j) {
         const int step = j < 8 ? 8 * dh + j : 16 + dh;
-        const bf16x8 v = *reinterpret_cast<const bf16x8*>(krow + 32 * step);
-        kreg[kbl][j] = kvalid ? v : bf16x8{};
-        // K_lat lives in the AGPR file (MFMA reads A/B operands from AGPRs directly): the arch
-        // VGPRs hold the 144 accumulators and the LDS operands in flight.
-        asm volatile("" : "+a"(kreg[kbl][j]));
+        kreg[kbl][j] = *reinterpret_cast<const bf16x8*>(krow + 32 * step);
       }
     }
+    // All 36 loads are issued before any is used (the scheduling barrier keeps them together):
+    // left to the scheduler, each load was awaited before the next was issued, 36 memory round
+    // trips in a row per segment.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kbl = 0; kbl < 4; ++kbl)
+      if (key0 + 16 * kbl + l16 >= p.Sk)
+#pragma unroll
+        for (int j = 0; j < 9; ++j) kreg[kbl][j] = bf16x8{};   // zero past Sk
+    // K_lat lives in the AGPR file (MFMA reads A/B operands from AGPRs directly): the arch VGPRs
+    // hold the 144 accumulators and the LDS operands in flight.
+#pragma unroll
+    for (int kbl = 0; kbl < 4; ++kbl)
+      asm volatile("" : "+a"(kreg[kbl][0]), "+a"(kreg[kbl][1]), "+a"(kreg[kbl][2]), "+a"(kreg[kbl][3]),
+                   "+a"(kreg[kbl][4]), "+a"(kreg[kbl][5]), "+a"(kreg[kbl][6]), "+a"(kreg[kbl][7]),
+                   "+a"(kreg[kbl][8]));
 
     f32x4 acc[4][9];
 #pragma unroll
