@@ -33,6 +33,9 @@
 // exactly.  A key that every later row of every head attends to sums thousands of such terms;
 // with bf16 P and dS' that rounding alone costs ~1e-3 of |dK_lat| (2e-2 at the config-5
 // magnitudes of ~20), with fp16 an eighth of it -- within a few 1e-3 of exact fp32 operands.
+// fp16's narrow exponent range is handled by a power-of-two gradient scale: dS' and dO enter the
+// fp16 products times 2^e, with e chosen on the device from the largest |dO| of the call, and
+// dq and dK_lat leave times 2^-e, so the relative error does not grow as dO gets small.
 #include <cstdlib>
 
 #include "dmla_common.h"
@@ -97,6 +100,8 @@ struct BwdParams {
                         // with lane c's 4 values at slot ds_slot(c)
   float* part;          // [n_items][2][4 kb][36 cb][64 lanes][4]: dK_lat partials in MFMA C order
   float* dk_acc;        // fp32 dK_lat of the chunks so far: [B][Sk][576], or the fp32 output itself
+  float* bmax;          // [B][n_rt]: largest |dO| of each bwd_prep workgroup
+  unsigned* gmax;       // largest |dO| of the call as fp32 bits (bwd_kt reduces bmax into it)
 };
 
 // ---- work split of the dK/dV kernel, shared by the host and the reduction ------------------
@@ -155,7 +160,8 @@ __device__ __forceinline__ f16x4 to_f16x4(float a, float b, float c, float d) {
 // ---- 1. row statistics -------------------------------------------------------------------
 // One workgroup per 32-row tile; 8 lanes per row.  Load c of lane p covers elements
 // 8 (8c + p) .. +7, so the 8 lanes of a row read 128 contiguous bytes per instruction, and
-// each lane keeps 16 loads in flight.
+// each lane keeps its 16 row loads and the row's m, l in flight together.  The workgroup also
+// records its largest |dO| for the gradient exponent.
 __global__ void __launch_bounds__(256) bwd_prep_kernel(BwdParams p) {
   const int b = blockIdx.y;
   const int t = threadIdx.x;
@@ -185,33 +191,42 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(BwdParams p) {
   }
   const int row = blockIdx.x * kRows + (t >> 3);
   const int part = t & 7;
-  float dsum = 0.f;
-  int pos = 0, h = 0;
   const bool valid = row < p.R;
-  if (valid) {
-    pos = fast_div(row, p.hdiv);
-    h = row - pos * p.H;
-    const bf16* orow = p.o + b * p.o_sb + h * p.o_sh + pos * p.o_ss + 8 * part;
-    const bf16* drow = p.dout + b * p.do_sb + h * p.do_sh + pos * p.do_ss + 8 * part;
-    bf16x8 ov[8], dv[8];
+  // Rows past R read row R - 1 (in bounds); their statistics are replaced below.
+  const int rr = valid ? row : p.R - 1;
+  const int pos = fast_div(rr, p.hdiv), h = rr - pos * p.H;
+  const bf16* orow = p.o + b * p.o_sb + h * p.o_sh + pos * p.o_ss + 8 * part;
+  const bf16* drow = p.dout + b * p.do_sb + h * p.do_sh + pos * p.do_ss + 8 * part;
+  const int64_t sidx = ((int64_t)b * p.H + h) * p.Sq + pos;
+  bf16x8 ov[8], dv[8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      ov[c] = *reinterpret_cast<const bf16x8*>(orow + 64 * c);
-      dv[c] = *reinterpret_cast<const bf16x8*>(drow + 64 * c);
-    }
-#pragma unroll
-    for (int c = 0; c < 8; ++c)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dsum += (float)ov[c][e] * (float)dv[c][e];
+  for (int c = 0; c < 8; ++c) {
+    ov[c] = *reinterpret_cast<const bf16x8*>(orow + 64 * c);
+    dv[c] = *reinterpret_cast<const bf16x8*>(drow + 64 * c);
   }
+  const float mv = p.m[sidx], lv = p.l[sidx];
+  // All 18 loads are in flight before the first is used: left to the scheduler, each group of
+  // loads was awaited before the next went out.
+  __builtin_amdgcn_sched_barrier(0);
+  float dsum = 0.f, amax = 0.f;
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = (float)dv[c][e];
+      dsum += (float)ov[c][e] * d;
+      amax = fmaxf(amax, fabsf(d));
+    }
+  // The block's largest |dO|, one value per workgroup; bwd_kt, launched next, reduces them into
+  // the call's maximum (the gradient exponent's input).
+  amax = workgroup_max256(amax);
+  if (t == 0) p.bmax[(int64_t)b * p.n_rt + blockIdx.x] = amax;
   dsum += __shfl_xor(dsum, 1, 8);
   dsum += __shfl_xor(dsum, 2, 8);
   dsum += __shfl_xor(dsum, 4, 8);
   if (part == 0) {
     float lse2 = __builtin_inff();
     if (valid) {
-      const int64_t idx = ((int64_t)b * p.H + h) * p.Sq + pos;
-      const float mv = p.m[idx], lv = p.l[idx];
       // Rows that see no key (l = 0) get +inf, so that P = exp2(s - lse2) = 0 everywhere.
       if (lv > 0.f && __builtin_isfinite(mv)) lse2 = (mv + __logf(lv)) * kLog2e;
     } else {
@@ -248,6 +263,8 @@ __global__ void __launch_bounds__(256) bwd_kt_kernel(BwdParams p) {
     for (int e = 0; e < 8; ++e) v[e] = tile[8 * c + e][d];
     *reinterpret_cast<f16x8*>(p.kt + ((int64_t)b * kDqk + 64 * db + d) * p.kt_ld + kb * 64 + 8 * c) = v;
   }
+  // The call's largest |dO| from bwd_prep's per-workgroup values (bwd_prep runs first).
+  if (db == 0 && kb == 0 && b == 0) reduce_max_bits(p.bmax, p.B * p.n_rt, p.gmax);
 }
 
 // ---- 3. dK_lat / dV: key-block-stationary sweep over row tiles ----------------------------
@@ -296,7 +313,9 @@ bwd_dkdv_kernel(BwdParams p) {
   const int rb = wave >> 1;      // S-phase row block
   const int dh = wave & 1;       // S-phase dim half; this wave finishes key blocks 2 dh, 2 dh + 1
   const int off = p.Sk - p.Sq;
-  const float scale = p.scale, scale_log2 = p.scale_log2;
+  const int gexp = grad_exponent(p.gmax);
+  const float scale = p.scale * exp2i(gexp), scale_log2 = p.scale_log2;   // dS' carries 2^e
+  const unsigned gexp_bits = grad_exponent_bits(gexp);   // dO operands: 2^e
   const unsigned lds_base = lds_addr(lds);
   DMLA_LDS char* xbuf = lds + kXOffset;
   DMLA_LDS char* xch = lds + kXchOffset;
@@ -516,7 +535,8 @@ bwd_dkdv_kernel(BwdParams p) {
       // Column operands of column block wave + 4v (v < 9: Q; v >= 9: dO block v - 9), as two
       // transposed half reads each.  Software pipeline over the 17 operands: step v issues the
       // reads of operand v + 3, the 4 MFMAs of operand v and, between them, the fp16
-      // conversion of operand v + 1, so each read has two steps (8 MFMAs) to land.  The
+      // conversion of operand v + 1 (a dO operand times 2^e, one more instruction per value
+      // pair), so each read has two steps (8 MFMAs) to land.  The
       // schedule is pinned with scheduling-group barriers: left to itself the compiler issued
       // each operand's reads right before its conversion and waited for them there, one LDS
       // round trip per operand.
@@ -537,7 +557,8 @@ bwd_dkdv_kernel(BwdParams p) {
           stage_copy(kQGroups + 2 * v + 1);
         }
         const f16x8 bop = bnext;
-        if (v + 1 < 17) bnext = bf16_to_f16(kl[(v + 1) & 3], kh[(v + 1) & 3]);
+        if (v + 1 < 9) bnext = bf16_to_f16(kl[(v + 1) & 3], kh[(v + 1) & 3]);
+        else if (v + 1 < 17) bnext = bf16_to_f16_scaled(kl[(v + 1) & 3], kh[(v + 1) & 3], gexp_bits);
         if (v < 9) {
 #pragma unroll
           for (int kbl = 0; kbl < 4; ++kbl) acc[kbl][v] = mfma_f16(dsT[kbl], bop, acc[kbl][v]);
@@ -549,7 +570,8 @@ bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // an MFMA of operand v
-          if (v + 1 < 17) __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // a quarter of the conversion
+          if (v + 1 < 9) __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // a quarter of the conversion
+          else if (v + 1 < 17) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
         }
         __builtin_amdgcn_sched_barrier(0);   // nothing crosses a step boundary
       }
@@ -663,7 +685,8 @@ __global__ void __launch_bounds__(kDqThreads, 1) bwd_dq_kernel(BwdParams p) {
     st = st == 2 ? 0 : st + 1;
   }
 
-  // acc[rq][v] holds dQ[row0 + 64 rh + 16 rq + 4 g + i][16 (wc + 4 v) + l16].
+  // acc[rq][v] holds dQ[row0 + 64 rh + 16 rq + 4 g + i][16 (wc + 4 v) + l16] times 2^e.
+  const float unscale = exp2i(-grad_exponent(p.gmax));
 #pragma unroll
   for (int rq = 0; rq < 4; ++rq) {
 #pragma unroll
@@ -675,8 +698,9 @@ __global__ void __launch_bounds__(kDqThreads, 1) bwd_dq_kernel(BwdParams p) {
 #pragma unroll
       for (int v = 0; v < 9; ++v) {
         const int col = 16 * (wc + 4 * v);
-        if (p.dq_fp32) static_cast<float*>(p.dq)[base + col] = acc[rq][v][i];
-        else static_cast<bf16*>(p.dq)[base + col] = (bf16)acc[rq][v][i];
+        const float x = acc[rq][v][i] * unscale;
+        if (p.dq_fp32) static_cast<float*>(p.dq)[base + col] = x;
+        else static_cast<bf16*>(p.dq)[base + col] = (bf16)x;
       }
     }
   }
@@ -714,6 +738,7 @@ __global__ void __launch_bounds__(256) bwd_dk_reduce_kernel(BwdParams p) {
 #pragma unroll
     for (int r = 0; r < kReduceSlots; ++r) s[r] += v[r];
   }
+  const float unscale = exp2i(-grad_exponent(p.gmax));   // the partials carry 2^e
 #pragma unroll
   for (int r = 0; r < kReduceSlots; ++r) {
     const int cb = (t >> 6) + 4 * r;
@@ -725,7 +750,7 @@ __global__ void __launch_bounds__(256) bwd_dk_reduce_kernel(BwdParams p) {
       const int64_t o = b * p.dk_sb + key * p.dk_ss + col;
       // Chunks after the first add to the fp32 sum of the earlier ones; the last writes dK_lat.
       const int64_t oa = p.dk_fp32 ? o : ((int64_t)b * p.Sk + key) * kDqk + col;
-      float v = s[r][i];
+      float v = s[r][i] * unscale;
       if (p.chunk > 0) v += p.dk_acc[oa];
       if (!p.last_chunk) p.dk_acc[oa] = v;
       else if (p.dk_fp32) static_cast<float*>(p.dk)[o] = v;
@@ -761,7 +786,7 @@ struct BwdPlan {
   int R, n_rt, n_kb, n_pairs, kt_ld, n_groups;
   int n_chunks, max_pairs, max_items;
   int64_t cap;     // dS' bytes per chunk, read once (ds_cap_bytes)
-  int64_t off_lsed, off_kt, off_goff, off_ds, off_part, off_acc, bytes;
+  int64_t off_lsed, off_kt, off_goff, off_bmax, off_gmax, off_ds, off_part, off_acc, bytes;
 };
 
 int64_t round256(int64_t x) { return (x + 255) & ~(int64_t)255; }
@@ -811,6 +836,8 @@ BwdPlan make_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int causal, int 
   pl.off_lsed = o; o += round256(B * pl.n_rt * kRows * 8);
   pl.off_kt = o;   o += round256(B * kDqk * (int64_t)pl.kt_ld * 2);
   pl.off_goff = o; o += round256(((int64_t)pl.n_groups + 1) * 4);
+  pl.off_bmax = o; o += round256(B * pl.n_rt * 4);
+  pl.off_gmax = o; o += 256;
   pl.off_ds = o;   o += round256(B * (int64_t)pl.max_pairs * kPairBytes);
   pl.off_part = o; o += round256((int64_t)pl.max_items * 2 * kPartFloats * 4);
   pl.off_acc = o;  o += pl.n_chunks > 1 ? round256(B * Sk * kDqk * 4) : 0;
@@ -895,6 +922,8 @@ extern "C" int dmla_bwd_cache_latent(const void* q, const void* k_lat, const voi
   p.lsed = reinterpret_cast<float2*>(ws + pl.off_lsed);
   p.kt = reinterpret_cast<_Float16*>(ws + pl.off_kt);
   p.goff = reinterpret_cast<int32_t*>(ws + pl.off_goff);
+  p.bmax = reinterpret_cast<float*>(ws + pl.off_bmax);
+  p.gmax = reinterpret_cast<unsigned*>(ws + pl.off_gmax);
   p.ds = reinterpret_cast<_Float16*>(ws + pl.off_ds);
   p.part = reinterpret_cast<float*>(ws + pl.off_part);
   p.dk_acc = dk_fp32 ? static_cast<float*>(dk_lat) : reinterpret_cast<float*>(ws + pl.off_acc);

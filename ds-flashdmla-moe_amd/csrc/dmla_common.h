@@ -56,6 +56,60 @@ __device__ __forceinline__ f16x8 bf16_to_f16(const bf16x4& lo, const bf16x4& hi)
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---- gradient exponent of the backward kernels ------------------------------------------------
+// Every gradient is linear in dO, so a backward may scale dO (and what is linear in it, such as
+// dS) by 2^e before an fp16 rounding and its results by 2^-e.  e >= 0 brings the largest |dO| of
+// the call to [4, 8), where fp16 operands keep their full 11-bit significand: small gradients
+// would otherwise land in fp16's subnormals.  e = 0 when max |dO| >= 4, which leaves every
+// result bit-identical to the unscaled computation.  gmax holds the fp32 bits of max |dO|.
+__device__ __forceinline__ int grad_exponent(const unsigned* gmax) {
+  const unsigned bits = *gmax;
+  const int ex = (int)(bits >> 23);
+  return bits == 0u || ex >= 0xff ? 0 : min(max(129 - ex, 0), 100);
+}
+__device__ __forceinline__ float exp2i(int e) { return __uint_as_float((unsigned)(127 + e) << 23); }
+// The c of bf16_to_f16_scaled for exponent e: adds e to the exponents of both values of a pair.
+__device__ __forceinline__ unsigned grad_exponent_bits(int e) { return ((unsigned)e << 23) | ((unsigned)e << 7); }
+
+// bf16 -> fp16 of 8 values times 2^e, c = grad_exponent_bits(e): one integer add per value pair
+// (no carry between the two values while the scaled exponents stay below 255, as they do for
+// |x| 2^e < 8).  A zero turns into 2^(e-127) (or its negative) before the conversion, which
+// rounds toward zero to a signed zero for e <= 100; so do bf16 subnormals.
+__device__ __forceinline__ f16x8 bf16_to_f16_scaled(const bf16x4& lo, const bf16x4& hi, unsigned c) {
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 a = __builtin_bit_cast(u32x2, lo) + c, b = __builtin_bit_cast(u32x2, hi) + c;
+  return bf16_to_f16(__builtin_bit_cast(bf16x4, a), __builtin_bit_cast(bf16x4, b));
+}
+
+// Maximum of v over a 256-thread workgroup, returned to every thread.  All threads must call
+// it, at most once per kernel (its LDS slots are not guarded against a second use).
+__device__ __forceinline__ float workgroup_max256(float v) {
+  __shared__ float wmax[4];
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+}
+
+// *gmax = fp32 bits of max(vals[0 .. n)) (values >= 0), by one 256-thread workgroup, eight
+// loads per thread and round.  Uses workgroup_max256.
+__device__ __forceinline__ void reduce_max_bits(const float* vals, int n, unsigned* gmax) {
+  float mx = 0.f;
+  for (int i0 = 0; i0 < n; i0 += 8 * 256) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = i0 + 256 * j + (int)threadIdx.x;
+      v[j] = i < n ? vals[i] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx = fmaxf(mx, v[j]);
+  }
+  mx = workgroup_max256(mx);
+  if (threadIdx.x == 0) *gmax = __float_as_uint(mx);
+}
+
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
 
 // The lane index, recomputed where it is called: the compiler can neither hoist it out of an

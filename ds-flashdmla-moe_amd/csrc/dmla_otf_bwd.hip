@@ -86,6 +86,8 @@ struct OtfBwdParams {
   bf16* dxlat;           // [4][B*H][Skp][64]: dK_lat hi, dK_lat lo, dV_lat hi, dV_lat lo
   float* wpart;          // [2][H][B*n_sc][128][64] fp32 partial weight gradients
   bf16* wt;              // [2][H][64][128]: WK^T, WV^T
+  float* bmax;           // [B*H][Sqp / 32]: largest |dO| of each prep workgroup
+  unsigned* gmax;        // largest |dO| of the call as fp32 bits (otf_bwd_wt reduces bmax into it)
 };
 
 __device__ __forceinline__ f16x8 to_f16(const bf16x8& x) {
@@ -157,13 +159,19 @@ __global__ void __launch_bounds__(256) otf_bwd_prep_kernel(OtfBwdParams p) {
   const int bh = blockIdx.y;
   const int b = bh / p.H, h = bh % p.H;
   const int r = blockIdx.x * 32 + (threadIdx.x >> 3), c = threadIdx.x & 7;
-  float dsum = 0.f;
+  float dsum = 0.f, amax = 0.f;
   if (r < p.Sq) {
     const bf16x8 ov = *reinterpret_cast<const bf16x8*>(p.o + b * p.o_sb + h * p.o_sh + (int64_t)r * p.o_ss + 8 * c);
     const bf16x8 dv = *reinterpret_cast<const bf16x8*>(p.dout + b * p.do_sb + h * p.do_sh + (int64_t)r * p.do_ss + 8 * c);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) dsum += (float)dv[e] * (float)ov[e];
+    for (int e = 0; e < 8; ++e) {
+      dsum += (float)dv[e] * (float)ov[e];
+      amax = fmaxf(amax, fabsf((float)dv[e]));
+    }
   }
+  // The block's largest |dO| (the gradient exponent's input); otf_bwd_wt reduces them.
+  amax = workgroup_max256(amax);
+  if (threadIdx.x == 0) p.bmax[(size_t)bh * (p.Sqp / 32) + blockIdx.x] = amax;
   dsum += __shfl_xor(dsum, 1);
   dsum += __shfl_xor(dsum, 2);
   dsum += __shfl_xor(dsum, 4);
@@ -192,6 +200,8 @@ __global__ void __launch_bounds__(256) otf_bwd_wt_kernel(OtfBwdParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) wt[(32 * (threadIdx.x & 1) + 8 * c + e) * kIn] = a[e];
   }
+  // The call's largest |dO| from the prep kernel's per-workgroup values (prep runs first).
+  if (h == 0 && x == 0) reduce_max_bits(p.bmax, p.B * p.H * (p.Sqp / 32), p.gmax);
 }
 
 // X_lat * mul of keys k0 + 16 kb + l16 (kb = 0, 1) as bf16 pairs (hi, lo), each in the layout
@@ -456,9 +466,13 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
   const int b = bh / p.H, h = bh % p.H;
   const int off = p.Sk - p.Sq;
   const int r0 = rblk * kRowBlk + 32 * wave;
-  f16x8 qreg[2][2], oreg[2][2];   // [rb][ks]: X[r0 + 16 rb + l16][32 ks + 8 g ..] as fp16
+  // dO, and with it dP, D, dS and dQ, carry 2^e (the gradient exponent) through the fp16 products.
+  const int gexp = grad_exponent(p.gmax);
+  const unsigned gexp_bits = grad_exponent_bits(gexp);
+  const float gscale = exp2i(gexp);
+  f16x8 qreg[2][2], oreg[2][2];   // [rb][ks]: X[r0 + 16 rb + l16][32 ks + 8 g ..] as fp16 (dO times 2^e)
   float lse[2];
-  f32x4 ndv[2];   // -D of row r0 + 16 rb + l16 in all four elements: the dP^T accumulator start
+  f32x4 ndv[2];   // -D 2^e of row r0 + 16 rb + l16 in all four elements: the dP^T accumulator start
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
     // Rows past Sq re-read row Sq-1: their lse2 is +inf, so their P is 0.
@@ -468,10 +482,12 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       qreg[rb][ks] = to_f16(*reinterpret_cast<const bf16x8*>(qrow + 32 * ks));
-      oreg[rb][ks] = to_f16(*reinterpret_cast<const bf16x8*>(orow + 32 * ks));
+      const bf16x8 ox = *reinterpret_cast<const bf16x8*>(orow + 32 * ks);
+      oreg[rb][ks] = bf16_to_f16_scaled(__builtin_shufflevector(ox, ox, 0, 1, 2, 3),
+                                        __builtin_shufflevector(ox, ox, 4, 5, 6, 7), gexp_bits);
     }
     lse[rb] = p.lse2[(size_t)bh * p.Sqp + r0 + 16 * rb + l16];
-    const float n = p.nd[(size_t)bh * p.Sqp + r0 + 16 * rb + l16];
+    const float n = p.nd[(size_t)bh * p.Sqp + r0 + 16 * rb + l16] * gscale;
     ndv[rb] = f32x4{n, n, n, n};
   }
   f32x4 dq[2][4];   // [rb][db]: dQ[r0 + 16 rb + 4 g + i][16 db + l16]
@@ -552,6 +568,7 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
     stage_iter(s, std::integral_constant<int, 0>{});
     if (s + 1 < n_st) stage_iter(s + 1, std::integral_constant<int, 1>{});
   }
+  const float unscale = kLn2 * exp2i(-gexp);   // scale / (scale log2 e), and 2^-e
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -561,7 +578,7 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
       const int64_t at = b * p.dq_sb + h * p.dq_sh + (int64_t)row * p.dq_ss + l16;
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const float v = dq[rb][db][i] * kLn2;   // scale / (scale log2 e)
+        const float v = dq[rb][db][i] * unscale;
         if (p.dq_fp32) static_cast<float*>(p.dq)[at + 16 * db] = v;
         else static_cast<bf16*>(p.dq)[at + 16 * db] = (bf16)v;
       }
@@ -707,7 +724,7 @@ __global__ void __launch_bounds__(256) otf_bwd_wreduce_kernel(OtfBwdParams p) {
 
 struct OtfBwdPlan {
   int Sqp, Skp, n_sc;
-  size_t off_lse2, off_nd, off_klat, off_vlat, off_dx, off_wpart, off_wt, bytes;
+  size_t off_lse2, off_nd, off_klat, off_vlat, off_dx, off_wpart, off_wt, off_bmax, off_gmax, bytes;
 };
 
 OtfBwdPlan make_otf_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk) {
@@ -725,6 +742,8 @@ OtfBwdPlan make_otf_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk) {
   pl.off_dx = o;    o += up(4 * keys * kLat * 2);
   pl.off_wpart = o; o += up((size_t)2 * H * B * pl.n_sc * kIn * kLat * sizeof(float));
   pl.off_wt = o;    o += up((size_t)2 * H * kIn * kLat * 2);
+  pl.off_bmax = o;  o += up(rows / 32 * sizeof(float));
+  pl.off_gmax = o;  o += 256;
   pl.bytes = o;
   return pl;
 }
@@ -830,6 +849,8 @@ extern "C" int dmla_bwd_onthefly(const void* q, const void* k, const void* v, co
   p.dxlat = reinterpret_cast<bf16*>(ws + pl.off_dx);
   p.wpart = reinterpret_cast<float*>(ws + pl.off_wpart);
   p.wt = reinterpret_cast<bf16*>(ws + pl.off_wt);
+  p.bmax = reinterpret_cast<float*>(ws + pl.off_bmax);
+  p.gmax = reinterpret_cast<unsigned*>(ws + pl.off_gmax);
 
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(otf_bwd_prep_kernel, dim3((unsigned)(pl.Sqp / 32), (unsigned)(B * H)), dim3(256), 0, s, p);

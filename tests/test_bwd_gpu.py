@@ -147,6 +147,23 @@ def test_bwd_is_deterministic(gpu):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("shift", [20, 40])
+def test_bwd_small_gradients_scale_exactly(gpu, shift):
+    """Gradients as small as training produces (|dO| ~ 1e-6 and far below).  The fp16 operands of
+    the second-stage products would turn such values into subnormals; the backward instead scales
+    dO and dS' by a power of two chosen on the device from max |dO| and the results back, so
+    dO 2^-shift yields exactly 2^-shift times the gradients of dO, bit for bit, and the parity of
+    the unscaled case carries over at every scale."""
+    q, k, do = _inputs(1, 16, 256, 256, seed=41)
+    small = (do.float() * 2.0 ** -shift).to(torch.bfloat16)   # exact: a power of two
+    _, _, _, dq, dk = _run(gpu, q, k, do, True)
+    _, _, _, dqs, dks = _run(gpu, q, k, small, True)
+    assert dk.abs().max().item() > 0.1
+    assert torch.equal(dqs.float() * 2.0 ** shift, dq.float()), "dq of a scaled dO"
+    assert torch.equal(dks * 2.0 ** shift, dk), "dk_lat of a scaled dO"
+
+
+@pytest.mark.gpu
 def test_autograd_function_matches_fp32_autograd(gpu):
     q, k, do = _inputs(1, 4, 96, 96, seed=31)
     qg = q.to(gpu).requires_grad_(True)

@@ -147,6 +147,21 @@ def test_otf_bwd_single_key_many_rows(gpu, B, H, Sq, causal):
 
 
 @pytest.mark.gpu
+def test_otf_bwd_small_gradients_scale_exactly(gpu):
+    """Gradients as small as training produces.  dQ's fp16 operands would turn dO ~ 1e-7 into
+    subnormals; the dQ kernel scales dO, D and dS by a power of two chosen on the device from
+    max |dO| and dQ back, and the dK/dV side keeps bf16's range, so dO 2^-24 yields exactly 2^-24
+    times every gradient of dO, bit for bit."""
+    xs = _inputs(1, 4, 256, 256, seed=43)
+    small = (xs[5].float() * 2.0 ** -24).to(torch.bfloat16)   # exact: a power of two
+    _, _, _, grads = _run(gpu, xs, True, **FP32)
+    _, _, _, grads_s = _run(gpu, xs[:5] + (small,), True, **FP32)
+    for name, a, b in zip(NAMES, grads, grads_s):
+        assert a.abs().max().item() > 0.01, name
+        assert torch.equal(b * 2.0 ** 24, a), f"{name} of a scaled dO"
+
+
+@pytest.mark.gpu
 def test_otf_bwd_single_token(gpu):
     """One key: softmax is constant, so the exact dq, dk and dwk are 0 and dS = dP - D is pure
     rounding (the recomputed V_lat against the bf16 O); they must stay small, while dv = dO and
