@@ -86,7 +86,7 @@ struct OtfBwdParams {
   bf16* dxlat;           // [4][B*H][Skp][64]: dK_lat hi, dK_lat lo, dV_lat hi, dV_lat lo
   float* wpart;          // [2][H][B*n_sc][128][64] fp32 partial weight gradients
   bf16* wt;              // [2][H][64][128]: WK^T, WV^T
-  float* bmax;           // [B*H][Sqp / 32]: largest |dO| of each prep workgroup
+  float* bmax;           // [B*H][Sqp / 128]: largest |dO| of each prep workgroup
   unsigned* gmax;        // largest |dO| of the call as fp32 bits (otf_bwd_wt reduces bmax into it)
 };
 
@@ -154,36 +154,58 @@ __device__ __forceinline__ void stage_pair(const void* x0, int64_t ss0, const vo
 }
 
 // ---------------------------------------------------------------------------------------------
-// Prep: one thread per 8 dims of a row; 32 rows per 256-thread block, grid (Sqp / 32, B*H).
+// Prep: one thread per 8 dims of four rows (32 apart); 128 rows per 256-thread block, grid
+// (Sqp / 128, B*H).  The eight row loads and the rows' m, l go out before any is used; O is read
+// only here, so its loads are non-temporal (they leave the cached lines of later kernels alone).
+// Rows past Sq re-read row Sq - 1 and are written as padding (+inf, 0).
 __global__ void __launch_bounds__(256) otf_bwd_prep_kernel(OtfBwdParams p) {
   const int bh = blockIdx.y;
   const int b = bh / p.H, h = bh % p.H;
-  const int r = blockIdx.x * 32 + (threadIdx.x >> 3), c = threadIdx.x & 7;
-  float dsum = 0.f, amax = 0.f;
-  if (r < p.Sq) {
-    const bf16x8 ov = *reinterpret_cast<const bf16x8*>(p.o + b * p.o_sb + h * p.o_sh + (int64_t)r * p.o_ss + 8 * c);
-    const bf16x8 dv = *reinterpret_cast<const bf16x8*>(p.dout + b * p.do_sb + h * p.do_sh + (int64_t)r * p.do_ss + 8 * c);
+  const int c = threadIdx.x & 7;
+  const int r0 = (int)blockIdx.x * kRowBlk + (int)(threadIdx.x >> 3);
+  bf16x8 ov[4], dv[4];
+  float mv[4], lv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = min(r0 + 32 * j, p.Sq - 1);
+    ov[j] = __builtin_nontemporal_load(
+        reinterpret_cast<const bf16x8*>(p.o + b * p.o_sb + h * p.o_sh + (int64_t)r * p.o_ss + 8 * c));
+    dv[j] = *reinterpret_cast<const bf16x8*>(p.dout + b * p.do_sb + h * p.do_sh + (int64_t)r * p.do_ss + 8 * c);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t idx = (int64_t)bh * p.Sq + min(r0 + 32 * j, p.Sq - 1);
+    mv[j] = p.m[idx];
+    lv[j] = p.l[idx];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float amax = 0.f, dsum[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    dsum[j] = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      dsum += (float)dv[e] * (float)ov[e];
-      amax = fmaxf(amax, fabsf((float)dv[e]));
+      dsum[j] += (float)dv[j][e] * (float)ov[j][e];
+      amax = fmaxf(amax, fabsf((float)dv[j][e]));
     }
   }
-  // The block's largest |dO| (the gradient exponent's input); otf_bwd_wt reduces them.
+  // The block's largest |dO| (the gradient exponent's input; re-read rows repeat a real row);
+  // otf_bwd_wt reduces them.
   amax = workgroup_max256(amax);
-  if (threadIdx.x == 0) p.bmax[(size_t)bh * (p.Sqp / 32) + blockIdx.x] = amax;
-  dsum += __shfl_xor(dsum, 1);
-  dsum += __shfl_xor(dsum, 2);
-  dsum += __shfl_xor(dsum, 4);
-  if (c == 0) {
-    float lse = __builtin_inff();   // P = 0 for padding rows and rows without keys
-    if (r < p.Sq) {
-      const int64_t idx = (int64_t)bh * p.Sq + r;
-      const float lv = p.l[idx];
-      if (lv > 0.f) lse = p.m[idx] * kLog2e + __builtin_log2f(lv);
+  if (threadIdx.x == 0) p.bmax[(size_t)bh * (p.Sqp / kRowBlk) + blockIdx.x] = amax;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float d = dsum[j];
+    d += __shfl_xor(d, 1);
+    d += __shfl_xor(d, 2);
+    d += __shfl_xor(d, 4);
+    const int r = r0 + 32 * j;
+    if (c == 0) {
+      float lse = __builtin_inff();   // P = 0 for padding rows and rows without keys
+      if (r < p.Sq && lv[j] > 0.f) lse = mv[j] * kLog2e + __builtin_log2f(lv[j]);
+      p.lse2[(size_t)bh * p.Sqp + r] = lse;
+      p.nd[(size_t)bh * p.Sqp + r] = r < p.Sq ? -d : 0.f;
     }
-    p.lse2[(size_t)bh * p.Sqp + r] = lse;
-    p.nd[(size_t)bh * p.Sqp + r] = -dsum;
   }
 }
 
@@ -201,7 +223,7 @@ __global__ void __launch_bounds__(256) otf_bwd_wt_kernel(OtfBwdParams p) {
     for (int e = 0; e < 8; ++e) wt[(32 * (threadIdx.x & 1) + 8 * c + e) * kIn] = a[e];
   }
   // The call's largest |dO| from the prep kernel's per-workgroup values (prep runs first).
-  if (h == 0 && x == 0) reduce_max_bits(p.bmax, p.B * p.H * (p.Sqp / 32), p.gmax);
+  if (h == 0 && x == 0) reduce_max_bits(p.bmax, p.B * p.H * (p.Sqp / kRowBlk), p.gmax);
 }
 
 // X_lat * mul of keys k0 + 16 kb + l16 (kb = 0, 1) as bf16 pairs (hi, lo), each in the layout
@@ -742,7 +764,7 @@ OtfBwdPlan make_otf_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk) {
   pl.off_dx = o;    o += up(4 * keys * kLat * 2);
   pl.off_wpart = o; o += up((size_t)2 * H * B * pl.n_sc * kIn * kLat * sizeof(float));
   pl.off_wt = o;    o += up((size_t)2 * H * kIn * kLat * 2);
-  pl.off_bmax = o;  o += up(rows / 32 * sizeof(float));
+  pl.off_bmax = o;  o += up(rows / kRowBlk * sizeof(float));
   pl.off_gmax = o;  o += 256;
   pl.bytes = o;
   return pl;
@@ -853,7 +875,7 @@ extern "C" int dmla_bwd_onthefly(const void* q, const void* k, const void* v, co
   p.gmax = reinterpret_cast<unsigned*>(ws + pl.off_gmax);
 
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(otf_bwd_prep_kernel, dim3((unsigned)(pl.Sqp / 32), (unsigned)(B * H)), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(otf_bwd_prep_kernel, dim3((unsigned)(pl.Sqp / kRowBlk), (unsigned)(B * H)), dim3(256), 0, s, p);
   hipLaunchKernelGGL(otf_bwd_wt_kernel, dim3((unsigned)H, 2), dim3(256), 0, s, p);
   hipLaunchKernelGGL(otf_bwd_dkdv_kernel, dim3((unsigned)grid_kv), dim3(256), 0, s, p);
   hipLaunchKernelGGL(otf_bwd_dq_kernel, dim3((unsigned)grid_q), dim3(256), 0, s, p);
