@@ -217,3 +217,14 @@ def test_decode_large_batch_uses_the_plan_kernel(gpu):
     o_ref, lse_ref = R.dmla_decode_paged(q.float(), pool.float(), table, sl, 512, SCALE)
     assert_out_close(o, o_ref)
     _lse_close(lse, lse_ref)   # empty sequences: lse -inf on both sides
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lens", [[131072], [1, 98304, 3]])
+def test_decode_one_very_long_context(gpu, lens):
+    """One sequence of 128K (or 96K beside two tiny ones) tokens: the plan splits it over every
+    workgroup, so a single sequence is merged from the most partials the combine ever sees."""
+    q, pool, table, sl = _paged(lens, 128, seed=len(lens) + 31, poison_tail=False)
+    plan = ops.flash_dmla_decode_plan(sl.to(gpu), 128, table.shape[1]).cpu().tolist()
+    assert max(R.plan_segment_pages(plan, lens)) <= 128
+    _check(gpu, q, pool, table, sl, oracle_device="gpu")
