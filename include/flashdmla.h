@@ -239,8 +239,11 @@ int dmla_lse_combine(const float* part_o, const float* part_lse, const int32_t* 
  *   gradient folded into the first d_v columns).  Rows with l = 0 contribute nothing.
  *   S = q K^T and dP = dout V^T use the bf16 inputs as they are; dS^T q, P^T dout and dS K
  *   take fp16 operands (P and dS rounded to fp16; q, dout, K converted to fp16, exact for
- *   magnitudes in fp16's normal range, saturating above 65504).  All products accumulate in
- *   fp32.
+ *   magnitudes in fp16's normal range, saturating above 65504).  dout and dS enter them
+ *   scaled by 2^e, the power of two (e >= 0, chosen on the device) that brings the call's
+ *   largest |dout| into [4, 8), and dq, dk_lat leave scaled back: small gradients keep fp16's
+ *   full precision, and dout 2^-s gives exactly 2^-s times the gradients of dout.  All
+ *   products accumulate in fp32.
  *   The result is deterministic (no atomics).  workspace: device memory of at least
  *   dmla_bwd_workspace_bytes(...) bytes for the same sizes on the current device, 16-byte
  *   aligned; its contents on entry do not matter.  The workspace grows linearly in Sq and Sk:
@@ -287,7 +290,8 @@ int dmla_bwd_cache_latent(const void* q, const void* k_lat, const void* o, const
  *   (and through it dk, dv, dwk, dwv) takes bf16 operands, every rounded one (K_lat, V_lat, P,
  *   dS, dK_lat, dV_lat) as a bf16 pair hi + lo (within 2^-16 relative); dq takes fp16 operands
  *   (q, dout converted exactly for magnitudes in fp16's normal range; K_lat, V_lat, dS rounded
- *   to fp16).  Deterministic (no atomics).  workspace: device memory of at least
+ *   to fp16), with dout and dS scaled by the same power of two as in dmla_bwd_cache_latent
+ *   and dq scaled back.  Deterministic (no atomics).  workspace: device memory of at least
  *   dmla_bwd_onthefly_workspace_bytes(...) bytes, 16-byte aligned; its contents on entry do not
  *   matter.
  * Supported: d_in = 128, d_lat = 64, 0 < Sq, Sk <= 2^24, row strides of q, dout, k, v below 2^24.
