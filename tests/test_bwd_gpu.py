@@ -164,6 +164,14 @@ def test_bwd_small_gradients_scale_exactly(gpu, shift):
 
 
 @pytest.mark.gpu
+def test_bwd_zero_output_gradient_gives_zero(gpu):
+    """dO = 0: the largest |dO| is 0, the gradient exponent stays 0, and every gradient is 0."""
+    q, k, do = _inputs(1, 16, 200, 200, seed=43)
+    _, _, _, dq, dk = _run(gpu, q, k, torch.zeros_like(do), True)
+    assert int(torch.count_nonzero(dq)) == 0 and int(torch.count_nonzero(dk)) == 0
+
+
+@pytest.mark.gpu
 def test_autograd_function_matches_fp32_autograd(gpu):
     q, k, do = _inputs(1, 4, 96, 96, seed=31)
     qg = q.to(gpu).requires_grad_(True)

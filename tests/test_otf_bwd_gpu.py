@@ -162,6 +162,15 @@ def test_otf_bwd_small_gradients_scale_exactly(gpu):
 
 
 @pytest.mark.gpu
+def test_otf_bwd_zero_output_gradient_gives_zero(gpu):
+    """dO = 0: every gradient of the on-the-fly backward is exactly 0."""
+    xs = _inputs(1, 2, 130, 130, seed=47)
+    _, _, _, grads = _run(gpu, xs[:5] + (torch.zeros_like(xs[5]),), True, **FP32)
+    for name, t in zip(NAMES, grads):
+        assert int(torch.count_nonzero(t)) == 0, name
+
+
+@pytest.mark.gpu
 def test_otf_bwd_single_token(gpu):
     """One key: softmax is constant, so the exact dq, dk and dwk are 0 and dS = dP - D is pure
     rounding (the recomputed V_lat against the bf16 O); they must stay small, while dv = dO and
