@@ -114,18 +114,32 @@ __global__ void __launch_bounds__(kOtfThreads, 1) otf_fwd_kernel(OtfParams p) {
   }
 
   // ---- raw K / V tile copies: 16 per tensor (4 keys x 256 B each), 4 per wave ----
-  // Copy n of tensor x (n < 16): keys 4n .. 4n+3; lane l -> key 4n + l/16, physical chunk l%16.
+  // Wave w copies tensor x = w / 4 (K, then V): copy c covers keys 4n .. 4n+3 with
+  // n = 4 (w % 4) + c; lane l -> key 4n + l/16 (= 16 (w % 4) + 4c + g), physical chunk
+  // l16 ^ (key % 16) = l16 ^ (4c + g).  The address is a wave-uniform base (the tile's first key
+  // plus 4c rows, scalar arithmetic) and a lane offset that does not change from tile to tile
+  // (row strides < 2^24 elements keep it below 2^31 bytes).  Computed per copy from 64-bit
+  // strides instead, the addresses had cost ~30 quarter-rate integer multiplies per wave and
+  // tile.  Only a tile that reaches past Sk takes per-lane addresses, clamped to the last key
+  // (those keys are masked).
+  const int xw = wave >> 2;
+  const bf16* xbase = xw == 0 ? p.k + b * p.k_sb + h * p.k_sh : p.v + b * p.v_sb + h * p.v_sh;
+  const int64_t xss = xw == 0 ? p.k_ss : p.v_ss;
+  const unsigned raw_lane = (unsigned)((16 * (wave & 3) + g) * xss * 2);
   auto stage_raw = [&](int t, int st) {
+    const unsigned ldst = lds_base + kRawOff + (st * 2 + xw) * kRawBytes + (wave & 3) * 4 * 1024;
+    if (t * kOtfKeys + kOtfKeys <= p.Sk) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int idx = wave * 4 + c;         // 0 .. 31
-      const int x = idx >> 4, n = idx & 15;
-      const int key = 4 * n + (lane >> 4);
-      const int gk = min(t * kOtfKeys + key, p.Sk - 1);   // keys past Sk re-read the last one (masked)
-      const int chunk = (lane & 15) ^ (key & 15);
-      const bf16* src = x == 0 ? p.k + b * p.k_sb + gk * p.k_ss + h * p.k_sh
-                               : p.v + b * p.v_sb + gk * p.v_ss + h * p.v_sh;
-      dma16_addr(src + 8 * chunk, lds_base + kRawOff + (st * 2 + x) * kRawBytes + n * 1024);
+      for (int c = 0; c < 4; ++c)
+        dma16(xbase + (int64_t)(t * kOtfKeys + 4 * c) * xss, raw_lane + 16u * (unsigned)(l16 ^ (4 * c + g)),
+              ldst + c * 1024);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int key = 16 * (wave & 3) + 4 * c + g;
+        const int gk = min(t * kOtfKeys + key, p.Sk - 1);
+        dma16_addr(xbase + (int64_t)gk * xss + 8 * (l16 ^ (4 * c + g)), ldst + c * 1024);
+      }
     }
   };
   if (n_t > 0) stage_raw(0, 0);
@@ -400,6 +414,8 @@ extern "C" int dmla_fwd_onthefly(const void* q, const void* k, const void* v, co
     return fail(DMLA_ERR_INVALID_ARG, "dmla_fwd_onthefly: input strides must be multiples of 8 elements");
   if (Sq > ((int64_t)1 << 30) || Sk > ((int64_t)1 << 30))
     return fail(DMLA_ERR_UNSUPPORTED, "dmla_fwd_onthefly: size too large");
+  if (k_ss < 0 || v_ss < 0 || k_ss >= ((int64_t)1 << 24) || v_ss >= ((int64_t)1 << 24))
+    return fail(DMLA_ERR_UNSUPPORTED, "dmla_fwd_onthefly: row strides of k and v must be in [0, 2^24)");
   if (B == 0 || H == 0 || Sq == 0) return DMLA_OK;
   OtfParams p = {};
   p.q = static_cast<const bf16*>(q);

@@ -87,7 +87,7 @@ int dmla_fwd_cache_latent(const void* q, const void* k_lat, void* o, float* m, f
  *   product as fp16 (V_lat saturates beyond |65504|).  Inputs must be finite: the kernel is
  *   built without NaN handling in its max reductions, so a NaN input gives unspecified (not
  *   necessarily NaN) outputs in the rows it reaches.
- * Supported: d_in = 128, d_lat = 64.
+ * Supported: d_in = 128, d_lat = 64, row strides of k and v below 2^24 elements.
  */
 int dmla_fwd_onthefly(const void* q, const void* k, const void* v, const void* wk, const void* wv,
                       void* o, float* m, float* l, int64_t B, int64_t H, int64_t Sq, int64_t Sk,

@@ -254,6 +254,23 @@ def test_same_device_check_names_the_tensors_on_other_devices():
         ops._same_device(q=a, k=b)
 
 
+def test_onthefly_forward_argument_errors():
+    lib = _lib.lib()
+    P = ctypes.c_void_p
+
+    def call(ks=128 * 2, vs=128 * 2, din=128, B=1):
+        ptrs = [P(1 << 20)] * 6 + [P(1 << 20), P(1 << 20)]
+        return lib.dmla_fwd_onthefly(*ptrs, B, 2, 64, 64, din, 64, 2 * 64 * 64, 64 * 64, 64,
+                                     64 * ks, ks, 128, 64 * vs, vs, 128, 128 * 64, 64,
+                                     2 * 64 * 64, 64 * 64, 64, 0.125, 1, None)
+
+    assert call(din=64) == _lib.DMLA_ERR_UNSUPPORTED
+    assert call(ks=1 << 24) == _lib.DMLA_ERR_UNSUPPORTED   # the copies' 32-bit lane offsets
+    assert call(vs=1 << 24) == _lib.DMLA_ERR_UNSUPPORTED
+    assert call(ks=2 * 128 + 4) == _lib.DMLA_ERR_INVALID_ARG
+    assert call(B=0) == _lib.DMLA_OK                        # empty: nothing launched
+
+
 def test_onthefly_forward_wrapper_takes_check_range():
     import inspect
     assert "check_range" in inspect.signature(ops.flash_dmla_fwd_onthefly).parameters
