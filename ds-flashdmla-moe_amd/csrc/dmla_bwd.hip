@@ -93,7 +93,9 @@ struct BwdParams {
   int rt_begin, rt_end; // this chunk's row tiles (group aligned)
   int chunk_pairs;      // (group, 64-key block) pairs of this chunk: dS' blocks per batch element
   int chunk, last_chunk;
-  float2* lsed;         // [B][32 n_rt] (lse2, D); padding rows hold (+inf, 0)
+  float4* rstat;        // [B][32 n_rt] (lse2, D, key limit as int bits, 0); padding rows (+inf, 0, -1)
+  int64_t* roff;        // [B][32 n_rt][2]: element offsets of the row's q and dout rows within the batch
+                        // element (those of the last row for padding rows)
   _Float16* kt;         // [B][576][kt_ld] fp16
   int32_t* goff;        // [n_groups + 1]: first (group, key block) pair of each group
   _Float16* ds;         // [B][chunk_pairs][8 row blocks][4 key blocks][256]: fp16 dS' 16x16 blocks, MFMA C order
@@ -234,7 +236,12 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(BwdParams p) {
     } else {
       dsum = 0.f;
     }
-    p.lsed[(int64_t)b * p.n_rt * kRows + row] = make_float2(lse2, dsum);
+    // The row's key limit (-1: no key) and its q / dout offsets, so that the dK/dV kernel's
+    // tile loop needs neither a division nor 64-bit stride products per row.
+    const int lim = valid ? (p.causal ? min(pos + (p.Sk - p.Sq), p.Sk - 1) : p.Sk - 1) : -1;
+    const int64_t ri = (int64_t)b * p.n_rt * kRows + row;
+    p.rstat[ri] = make_float4(lse2, dsum, __int_as_float(lim), 0.f);
+    *reinterpret_cast<longlong2*>(p.roff + 2 * ri) = make_longlong2(h * p.q_sh + pos * p.q_ss, h * p.do_sh + pos * p.do_ss);
   }
 }
 
@@ -314,7 +321,6 @@ bwd_dkdv_kernel(BwdParams p) {
   const int l16 = lane & 15, g = lane >> 4;
   const int rb = wave >> 1;      // S-phase row block
   const int dh = wave & 1;       // S-phase dim half; this wave finishes key blocks 2 dh, 2 dh + 1
-  const int off = p.Sk - p.Sq;
   const int gexp = grad_exponent(p.gmax);
   const float scale = p.scale * exp2i(gexp), scale_log2 = p.scale_log2;   // dS' carries 2^e
   const unsigned gexp_bits = grad_exponent_bits(gexp);   // dO operands: 2^e
@@ -399,11 +405,23 @@ bwd_dkdv_kernel(BwdParams p) {
     const char* qsrc = nullptr;
     const char* osrc = nullptr;
     unsigned cdst = 0;
-    auto stage_begin = [&](int rt, int st) {
+    // The segment's first tile from the row index; the later ones from the offsets bwd_prep
+    // stored for each row (loaded a tile ahead with the statistics), which spares the tile loop
+    // a division and four 64-bit stride products per lane.
+    auto stage_begin_first = [&](int rt, int st) {
       const int r = min(rt * kRows + crow, p.R - 1);
       const int pos = fast_div(r, p.hdiv), h = r - pos * p.H;
       qsrc = reinterpret_cast<const char*>(p.q + b * p.q_sb + h * p.q_sh + pos * p.q_ss + 8 * cchunk);
       osrc = reinterpret_cast<const char*>(p.dout + b * p.do_sb + h * p.do_sh + pos * p.do_ss + 8 * cchunk);
+      cdst = lds_base + st * kStageBytes + wave * 1024;
+    };
+    longlong2 roff_next = {};   // q / dout offsets of the copy row of the tile staged next
+    auto roff_load = [&](int rt) {
+      roff_next = *reinterpret_cast<const longlong2*>(p.roff + 2 * ((int64_t)b * p.n_rt * kRows + rt * kRows + crow));
+    };
+    auto stage_begin = [&](int st) {
+      qsrc = reinterpret_cast<const char*>(p.q + b * p.q_sb + roff_next.x + 8 * cchunk);
+      osrc = reinterpret_cast<const char*>(p.dout + b * p.do_sb + roff_next.y + 8 * cchunk);
       cdst = lds_base + st * kStageBytes + wave * 1024;
     };
     auto stage_copy = [&](int i) {   // i < 9: Q chunk group i; else dO chunk group i - 9
@@ -419,22 +437,21 @@ bwd_dkdv_kernel(BwdParams p) {
     auto row_stats = [&](int rt) {
       ds_pair = (int64_t)b * p.chunk_pairs + p.goff[rt >> 2] - goff0 + kb;
       const int r0 = rt * kRows + 16 * rb + 4 * g;
-      const float4* src = reinterpret_cast<const float4*>(p.lsed + (int64_t)b * p.n_rt * kRows + r0);
-      const float4 a0 = src[0], a1 = src[1];
-      lse2[0] = a0.x; dval[0] = a0.y; lse2[1] = a0.z; dval[1] = a0.w;
-      lse2[2] = a1.x; dval[2] = a1.y; lse2[3] = a1.z; dval[3] = a1.w;
+      const float4* src = p.rstat + (int64_t)b * p.n_rt * kRows + r0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = r0 + i;
-        const int pos = fast_div(r, p.hdiv);
-        lim[i] = r >= p.R ? -1 : (p.causal ? min(pos + off, p.Sk - 1) : p.Sk - 1);
+        const float4 a = src[i];
+        lse2[i] = a.x;
+        dval[i] = a.y;
+        lim[i] = __float_as_int(a.z);
       }
     };
 
-    stage_begin(rt_first, 0);
+    stage_begin_first(rt_first, 0);
 #pragma unroll
     for (int i = 0; i < kQGroups + kOGroups; ++i) stage_copy(i);
     row_stats(rt_first);
+    roff_load(count > 1 ? rt_first + dir : rt_first);
     for (int s = 0; s < count; ++s) {
       const int rt = rt_first + dir * s;
       const int st = s & 1;
@@ -443,7 +460,7 @@ bwd_dkdv_kernel(BwdParams p) {
       const bool more = s + 1 < count;
       // The copies run unconditionally (branch-free loop body): past the segment's last tile they
       // re-read this tile into the idle stage, and the segment end waits for them.
-      stage_begin(more ? rt + dir : rt, st ^ 1);
+      stage_begin(st ^ 1);   // tile s + 1, or tile s again past the segment's last
       const DMLA_LDS char* qt = lds + st * kStageBytes;
       const DMLA_LDS char* ot = qt + kQBytes;
 
@@ -520,7 +537,10 @@ bwd_dkdv_kernel(BwdParams p) {
         *reinterpret_cast<f16x4*>(dsblk + 4 * ds_slot(lane)) = db;
       }
       __syncthreads();   // exchange written
-      if (more) row_stats(rt + dir);
+      if (more) {
+        row_stats(rt + dir);
+        roff_load(s + 2 < count ? rt + 2 * dir : rt + dir);   // the tile the next iteration stages
+      }
 
       // ---- dK-phase ----
       f16x8 pT[4], dsT[4];
@@ -788,7 +808,7 @@ struct BwdPlan {
   int R, n_rt, n_kb, n_pairs, kt_ld, n_groups;
   int n_chunks, max_pairs, max_items;
   int64_t cap;     // dS' bytes per chunk, read once (ds_cap_bytes)
-  int64_t off_lsed, off_kt, off_goff, off_bmax, off_gmax, off_ds, off_part, off_acc, bytes;
+  int64_t off_rstat, off_roff, off_kt, off_goff, off_bmax, off_gmax, off_ds, off_part, off_acc, bytes;
 };
 
 int64_t round256(int64_t x) { return (x + 255) & ~(int64_t)255; }
@@ -835,7 +855,8 @@ BwdPlan make_plan(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int causal, int 
     g0 = c.g1;
   }
   int64_t o = 0;
-  pl.off_lsed = o; o += round256(B * pl.n_rt * kRows * 8);
+  pl.off_rstat = o; o += round256(B * pl.n_rt * kRows * 16);
+  pl.off_roff = o; o += round256(B * pl.n_rt * kRows * 16);
   pl.off_kt = o;   o += round256(B * kDqk * (int64_t)pl.kt_ld * 2);
   pl.off_goff = o; o += round256(((int64_t)pl.n_groups + 1) * 4);
   pl.off_bmax = o; o += round256(B * pl.n_rt * 4);
@@ -921,7 +942,8 @@ extern "C" int dmla_bwd_cache_latent(const void* q, const void* k_lat, const voi
   p.R = pl.R; p.n_rt = pl.n_rt; p.n_kb = pl.n_kb; p.n_pairs = pl.n_pairs;
   p.kt_ld = pl.kt_ld; p.n_groups = pl.n_groups;
   char* ws = static_cast<char*>(workspace);
-  p.lsed = reinterpret_cast<float2*>(ws + pl.off_lsed);
+  p.rstat = reinterpret_cast<float4*>(ws + pl.off_rstat);
+  p.roff = reinterpret_cast<int64_t*>(ws + pl.off_roff);
   p.kt = reinterpret_cast<_Float16*>(ws + pl.off_kt);
   p.goff = reinterpret_cast<int32_t*>(ws + pl.off_goff);
   p.bmax = reinterpret_cast<float*>(ws + pl.off_bmax);
