@@ -413,8 +413,11 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
   };
 
   // One stage; the buffer index is a compile-time constant (the loop below is unrolled by two)
-  // so that every LDS address is a lane offset plus an instruction immediate.
-  auto stage_iter = [&](int s, auto buf_tag) {
+  // so that every LDS address is a lane offset plus an instruction immediate.  kAny: the stage
+  // may hold sub-tiles to skip or to mask, each picked at run time; otherwise every sub-tile
+  // takes the unmasked body with no branch (padding rows past Sq contribute 0: their P is 0
+  // through lse2 = +inf).
+  auto stage_iter = [&](int s, auto buf_tag, auto any_tag) {
     constexpr int kBuf = decltype(buf_tag)::value;
     wait_vmem();
     __syncthreads();   // stage s complete; every wave is done with stage s-1
@@ -423,17 +426,35 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int r0 = rs0 + 64 * s + 32 * t;
-      if (r0 >= p.Sq || (p.causal && k0 > r0 + 31 + off)) continue;   // padding only / all masked
-      if (k0 + 31 >= p.Sk || (p.causal && k0 + 31 > r0 + off))
-        subtile(st + t * kTile, st + (2 + t) * kTile, st + kStage + 128 * t, r0, std::true_type{});
-      else
+      if constexpr (decltype(any_tag)::value) {
+        if (r0 >= p.Sq || (p.causal && k0 > r0 + 31 + off)) continue;   // padding only / all masked
+        if (k0 + 31 >= p.Sk || (p.causal && k0 + 31 > r0 + off))
+          subtile(st + t * kTile, st + (2 + t) * kTile, st + kStage + 128 * t, r0, std::true_type{});
+        else
+          subtile(st + t * kTile, st + (2 + t) * kTile, st + kStage + 128 * t, r0, std::false_type{});
+      } else {
         subtile(st + t * kTile, st + (2 + t) * kTile, st + kStage + 128 * t, r0, std::false_type{});
+      }
     }
   };
+  // The stages near the diagonal (and all of them in a key block reaching past Sk) come first,
+  // an even number of them; from there on no sub-tile of any wave needs a mask.  Alternating
+  // between the two bodies inside one loop had the compiler copy the 64 dK/dV accumulator
+  // registers at every join.
+  const int key_last = kblk * kKeyBlk + kKeyBlk - 1;   // the workgroup's last key
+  int s_split = n_st;
+  if (key_last < p.Sk) s_split = p.causal ? max(0, (key_last - off - rs0 + 63) / 64) : 0;
+  s_split = min(n_st, (s_split + 1) & ~1);
+  using Any = std::true_type;
+  using Clean = std::false_type;
   if (n_st > 0) stage_rows(rs0, lbase);
-  for (int s = 0; s < n_st; s += 2) {
-    stage_iter(s, std::integral_constant<int, 0>{});
-    if (s + 1 < n_st) stage_iter(s + 1, std::integral_constant<int, 1>{});
+  for (int s = 0; s < s_split; s += 2) {
+    stage_iter(s, std::integral_constant<int, 0>{}, Any{});
+    if (s + 1 < n_st) stage_iter(s + 1, std::integral_constant<int, 1>{}, Any{});
+  }
+  for (int s = s_split; s < n_st; s += 2) {
+    stage_iter(s, std::integral_constant<int, 0>{}, Clean{});
+    if (s + 1 < n_st) stage_iter(s + 1, std::integral_constant<int, 1>{}, Clean{});
   }
   // dK_lat = scale dS^T Q and dV_lat = P^T dO as bf16 hi / lo planes (keys past Sk hold zeros:
   // P = 0 there)
