@@ -589,8 +589,10 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
       for (int rb = 0; rb < 2; ++rb) dq[rb][db] = mfma_f16(dsa[rb], kcol[db], dq[rb][db]);
   };
 
-  // Unrolled by two stages so that the buffer offset is an instruction immediate.
-  auto stage_iter = [&](int s, auto buf_tag) {
+  // Unrolled by two stages so that the buffer offset is an instruction immediate.  kAny: the
+  // stage may hold sub-tiles to skip or to mask, picked at run time; otherwise every sub-tile
+  // takes the unmasked body with no branch.
+  auto stage_iter = [&](int s, auto buf_tag, auto any_tag) {
     constexpr int kBuf = decltype(buf_tag)::value;
     wait_vmem();
     __syncthreads();
@@ -599,17 +601,32 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int c0 = 64 * s + 32 * t;
-      if (c0 >= key_end || (p.causal && c0 > r0 + 31 + off)) continue;
-      if (c0 + 31 >= p.Sk || (p.causal && c0 + 31 > r0 + off))
-        subtile(st + t * kTile, st + (2 + t) * kTile, c0, std::true_type{});
-      else
+      if constexpr (decltype(any_tag)::value) {
+        if (c0 >= key_end || (p.causal && c0 > r0 + 31 + off)) continue;
+        if (c0 + 31 >= p.Sk || (p.causal && c0 + 31 > r0 + off))
+          subtile(st + t * kTile, st + (2 + t) * kTile, c0, std::true_type{});
+        else
+          subtile(st + t * kTile, st + (2 + t) * kTile, c0, std::false_type{});
+      } else {
         subtile(st + t * kTile, st + (2 + t) * kTile, c0, std::false_type{});
+      }
     }
   };
+  // The stages whose keys every row of the block sees come first, an even number of them; the
+  // ones reaching the diagonal (or past Sk) follow.  With both sub-tile bodies in one loop, the
+  // compiler had copied the 32 dQ accumulator registers at every join.
+  const int lim_all = min(min(p.Sk, key_end) - 1, p.causal ? rblk * kRowBlk + off : p.Sk);
+  const int s_split = min(n_st, lim_all >= 0 ? ((lim_all + 1) / 64) & ~1 : 0);
+  using Any = std::true_type;
+  using Clean = std::false_type;
   if (n_st > 0) stage_pair(ksrc, kLat, vsrc, kLat, 0, p.Skp, lbase, wave, lane);
-  for (int s = 0; s < n_st; s += 2) {
-    stage_iter(s, std::integral_constant<int, 0>{});
-    if (s + 1 < n_st) stage_iter(s + 1, std::integral_constant<int, 1>{});
+  for (int s = 0; s < s_split; s += 2) {
+    stage_iter(s, std::integral_constant<int, 0>{}, Clean{});
+    if (s + 1 < n_st) stage_iter(s + 1, std::integral_constant<int, 1>{}, Clean{});
+  }
+  for (int s = s_split; s < n_st; s += 2) {
+    stage_iter(s, std::integral_constant<int, 0>{}, Any{});
+    if (s + 1 < n_st) stage_iter(s + 1, std::integral_constant<int, 1>{}, Any{});
   }
   const float unscale = kLn2 * exp2i(-gexp);   // scale / (scale log2 e), and 2^-e
 #pragma unroll
