@@ -11,7 +11,7 @@
 // Rows are (query position, head) pairs with the head fastest, as in the forward, so the 16
 // heads of a position share one causal key range.  Five kernels run in order on one stream:
 //   bwd_prep_kernel       per row: lse2 = (m + ln l) log2(e) and D = rowsum(dO * O);
-//   bwd_kt_kernel         K_lat^T in fp16 (dims x keys, zero padded): the B operand of dQ = dS' K;
+//   bwd_kt_kernel         K_lat^T in fp16 (32-key tiles of dims x keys, zero padded): dQ's B operand;
 //   bwd_dkdv_kernel       per 64-key block, streaming 32-row tiles: S, P, dP and dS' = scale dS
 //                         on MFMA, dK_lat accumulated in registers (V fold included), dS'
 //                         written once to HBM as fp16 16x16 blocks;
@@ -96,7 +96,7 @@ struct BwdParams {
   float4* rstat;        // [B][32 n_rt] (lse2, D, key limit as int bits, 0); padding rows (+inf, 0, -1)
   int64_t* roff;        // [B][32 n_rt][2]: element offsets of the row's q and dout rows within the batch
                         // element (those of the last row for padding rows)
-  _Float16* kt;         // [B][576][kt_ld] fp16
+  _Float16* kt;         // [B][kt_ld / 32][576][32] fp16: K^T in 32-key tiles, each tile contiguous
   int32_t* goff;        // [n_groups + 1]: first (group, key block) pair of each group
   _Float16* ds;         // [B][chunk_pairs][8 row blocks][4 key blocks][256]: fp16 dS' 16x16 blocks, MFMA C order
                         // with lane c's 4 values at slot ds_slot(c)
@@ -270,7 +270,9 @@ __global__ void __launch_bounds__(256) bwd_kt_kernel(BwdParams p) {
     f16x8 v;
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = tile[8 * c + e][d];
-    *reinterpret_cast<f16x8*>(p.kt + ((int64_t)b * kDqk + 64 * db + d) * p.kt_ld + kb * 64 + 8 * c) = v;
+    // 32-key tile 2 kb + c / 4, keys 8 (c % 4) .. +7 of its dim row 64 db + d
+    const int64_t tile_idx = (int64_t)b * (p.kt_ld / 32) + 2 * kb + (c >> 2);
+    *reinterpret_cast<f16x8*>(p.kt + (tile_idx * kDqk + 64 * db + d) * 32 + 8 * (c & 3)) = v;
   }
   // The call's largest |dO| from bwd_prep's per-workgroup values (bwd_prep runs first).
   if (db == 0 && kb == 0 && b == 0) reduce_max_bits(p.bmax, p.B * p.n_rt, p.gmax);
@@ -638,10 +640,19 @@ __global__ void __launch_bounds__(kDqThreads, 1) bwd_dq_kernel(BwdParams p) {
   const int n_rb = 2 * p.n_rt;
 
   // Copies.  dS': wave w moves row block w of the group, key blocks 2 kt, 2 kt + 1 (1 KB contiguous).
-  // K^T: 16 dims x 32 keys per copy (1 KB), wave w copies dim blocks w, w+8, .. (5 or 4 copies);
-  // lane l -> dim 16 n + l/4, physical chunk l%4 = logical chunk (l%4) ^ (l/16).
-  const unsigned kt_voff = (unsigned)(((lane >> 2) * p.kt_ld + 8 * ((lane & 3) ^ (lane >> 4))) * 2);
-  // Every wave issues exactly kDqCopies copies per stage (so one vmcnt value waits for a stage):
+  // K^T: 16 dims x 32 keys per copy (1 KB, contiguous in the tiled K^T: whole 128-byte lines
+  // per copy, where rows of a dims x keys matrix gave 64-byte pieces of 16 lines), wave w copies
+  // dim blocks w, w+8, .. (5 or 4 copies);
+  // lane l -> dim row r = l/4 of block n, physical chunk l%4 = logical chunk (l%4) ^ kt_swz(r).
+  // A ds_read_b128 is served 16 lanes at a time, the lanes with equal bit 5 and equal parity of
+  // bits 2-4 of the lane index (a model that predicts the LDS bank-conflict counter for every
+  // swizzle of the form parity(r & m0) | parity(r & m1) << 1 of this read).  In the read below
+  // such a group holds rows r, r^12 of one column group g and rows r^4, r^8 of g^1, all on the
+  // same 16 banks of the 64 (64-byte rows), so their four chunks must differ: kt_swz(r) = 2 *
+  // bit 2 of r does that.  Swizzled by r >> 2, every K^T read was a two-way conflict.
+  auto kt_swz = [](int r) { return 2 * ((r >> 2) & 1); };
+  const unsigned kt_voff = (unsigned)(((lane >> 2) * 32 + 8 * ((lane & 3) ^ kt_swz(lane >> 2))) * 2);
+  // Every wave issues exactly six copies per stage (so one vmcnt value waits for a stage):
   // a row block past the buffer copies row block 0 instead (its rows are not stored), and
   // waves 4-7 copy their dim block w + 24 a second time (same bytes to the same place).
   const int rblk = 8 * t + wave < n_rb ? wave : 0;
@@ -654,7 +665,7 @@ __global__ void __launch_bounds__(kDqThreads, 1) bwd_dq_kernel(BwdParams p) {
     } else {
       const int n0 = wave + 8 * (m - 1);
       const int n = n0 < kDqk / 16 ? n0 : n0 - 8;
-      const _Float16* ksrc = p.kt + ((int64_t)b * kDqk + 16 * n) * p.kt_ld + 32 * kt;
+      const _Float16* ksrc = p.kt + (((int64_t)b * (p.kt_ld / 32) + kt) * kDqk + 16 * n) * 32;
       dma16(ksrc, kt_voff, dst + kDqDsBytes + n * 1024);
     }
   };
@@ -669,7 +680,7 @@ __global__ void __launch_bounds__(kDqThreads, 1) bwd_dq_kernel(BwdParams p) {
   const int a_off0 = 4 * rh * 1024 + (g >> 1) * 512 + 8 * ds_slot(a_c);
   const int a_off1 = 4 * rh * 1024 + (g >> 1) * 512 + 8 * ds_slot(a_c + 4);
   // K^T B operand of column block wc + 4u: dim row 16 cb + l16, logical chunk g.
-  const int b_off = kDqDsBytes + wc * 1024 + l16 * 64 + 16 * (g ^ e);
+  const int b_off = kDqDsBytes + wc * 1024 + l16 * 64 + 16 * (g ^ kt_swz(l16));
 
   f32x4 acc[4][9];
 #pragma unroll
