@@ -498,8 +498,10 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
 //   dS^T = P^T (dP^T - D)
 //   dQ += dS K_lat                        (A = dS straight from the C tiles of S^T; B = K_lat by
 //                                          transposed reads, keys in the same order)
-// Grid: row blocks heavy (last) first.
-__global__ void __launch_bounds__(256, 2) otf_bwd_dq_kernel(OtfBwdParams p) {
+// Grid: row blocks heavy (last) first.  Three workgroups per CU (168 registers, 32 KB of LDS
+// each): a sub-tile is one dependent chain (S and dP, then exp2 and dS, then the dQ MFMAs), and
+// a third wave per SIMD covers more of its latency than two (191 -> 184 us at the cfg-4 shapes).
+__global__ void __launch_bounds__(256, 3) otf_bwd_dq_kernel(OtfBwdParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
   DMLA_LDS char* lds = (DMLA_LDS char*)smem;
   const int wave = uniform(threadIdx.x >> 6), lane = lane_id(), l16 = lane & 15, g = lane >> 4;
