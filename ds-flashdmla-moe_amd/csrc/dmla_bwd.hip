@@ -58,7 +58,7 @@ constexpr int kDkdvLds = kXOffset + 2 * 4 * 1024 + 4 * 4096;   // 160 KB: stages
 constexpr int kCb = kDqk / 16;                      // 36 column blocks of dK / dQ
 constexpr int kPartFloats = kKeys * kDqk;           // one dK partial: 64 keys x 576 fp32
 constexpr int kMaxParts = 64;
-// dQ kernel: stage = dS' blocks of 64 rows x 32 keys (4 KB) + K^T of 576 dims x 32 keys (36 KB)
+// dQ kernel: stage = dS' blocks of 128 rows x 32 keys (8 KB) + K^T of 576 dims x 32 keys (36 KB)
 constexpr int kDqRows = 128;                        // rows per dQ workgroup (8 waves, two row halves)
 constexpr int kDqThreads = 512;
 constexpr int kDqDsBytes = 8192;
@@ -88,7 +88,7 @@ struct BwdParams {
   int n_pairs;          // ceil(n_kb / 2)
   int parts;            // row segments per key-block pair (this chunk)
   int n_items;          // B * n_pairs * parts
-  int kt_ld;            // K^T row length (keys): 64 * n_kb
+  int kt_ld;            // keys K^T covers (zero padded): 64 * n_kb, kt_ld / 32 tiles
   int n_groups;         // 128-row groups: ceil(n_rt / 4)
   int rt_begin, rt_end; // this chunk's row tiles (group aligned)
   int chunk_pairs;      // (group, 64-key block) pairs of this chunk: dS' blocks per batch element
