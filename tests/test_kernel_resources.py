@@ -1,4 +1,4 @@
-"""Register-spill guard for the hot forward kernels (CPU only: compiles, runs nothing).
+"""Register-spill and occupancy guards for the hot kernels (CPU only: compiles, runs nothing).
 
 The cache-latent prefill and the paged decode share `mqa_fwd_kernel`.  Scratch traffic inside
 its tile loop costs every tile, and outside it a spill reload is followed by a `vmcnt` wait
@@ -62,3 +62,38 @@ def test_forward_tile_loops_are_spill_free(tmp_path):
                 assert not scratch, f"kernel {decode}: scratch access in a tile iteration: {scratch[:2]}"
         far = [i for i, l in enumerate(ins) if l.startswith("scratch_") and all(abs(i - c) > 40 for c in calls)]
         assert len(far) <= 4, f"kernel {decode}: {len(far)} scratch accesses outside the exact-path call"
+
+
+# Occupancy each backward kernel's tuning assumes (waves per SIMD the compiler reports for it):
+# the on-the-fly dQ kernel runs three workgroups per CU (a third wave per SIMD covers more of
+# its sub-tiles' dependent chain), the others two, and the cache-latent dK/dV kernel one wave
+# per SIMD with its 512 registers.  None of them may spill.
+_BWD_OCCUPANCY = {
+    "dmla_bwd.hip": {"bwd_dkdv_kernel": 1, "bwd_dq_kernel": 2},
+    "dmla_otf_bwd.hip": {"otf_bwd_dkdv_kernel": 2, "otf_bwd_dq_kernel": 3, "otf_bwd_wgrad_kernel": 2},
+}
+
+
+def _kernel_stats(asm):
+    """kernel short name -> (VGPRs, scratch bytes, occupancy) from the compiler's comments."""
+    stats = {}
+    for m in re.finditer(r"^_ZN4dmla\S*?((?:otf_)?bwd_[a-z_]+?_kernel)\S*:", asm, re.M):
+        rest = asm[m.end():]
+        get = lambda key: int(re.search(r"; %s: (\d+)" % key, rest).group(1))
+        stats[m.group(1)] = (get("NumVgprs"), get("ScratchSize"), get("Occupancy"))
+    return stats
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is needed")
+@pytest.mark.parametrize("source", sorted(_BWD_OCCUPANCY))
+def test_backward_kernels_keep_occupancy_without_spills(tmp_path, source):
+    out = tmp_path / (source + ".s")
+    run = subprocess.run([HIPCC] + FLAGS + [os.path.join(CSRC, source), "-o", str(out)],
+                         capture_output=True, text=True, timeout=600)
+    assert run.returncode == 0, run.stderr[-2000:]
+    stats = _kernel_stats(out.read_text())
+    for name, (vgprs, scratch, occupancy) in stats.items():
+        assert scratch == 0, f"{name}: {scratch} bytes of scratch ({vgprs} VGPRs)"
+    for name, want in _BWD_OCCUPANCY[source].items():
+        assert name in stats, f"{name} not found in {source}"
+        assert stats[name][2] >= want, f"{name}: occupancy {stats[name][2]} < {want} ({stats[name][0]} VGPRs)"
