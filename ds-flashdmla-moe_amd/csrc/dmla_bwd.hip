@@ -77,6 +77,7 @@ struct BwdParams {
   void* dq;
   void* dk;
   int dq_fp32, dk_fp32;
+  int dq_rows16;        // bf16 dq whose strides are multiples of 8 elements: stored as whole rows
   int64_t q_sb, q_sh, q_ss, k_sb, k_ss, o_sb, o_sh, o_ss, do_sb, do_sh, do_ss;
   int64_t dq_sb, dq_sh, dq_ss, dk_sb, dk_ss;
   int B, H, Sq, Sk, causal;
@@ -720,6 +721,45 @@ __global__ void __launch_bounds__(kDqThreads, 1) bwd_dq_kernel(BwdParams p) {
 
   // acc[rq][v] holds dQ[row0 + 64 rh + 16 rq + 4 g + i][16 (wc + 4 v) + l16] times 2^e.
   const float unscale = exp2i(-grad_exponent(p.gmax));
+  if (p.dq_rows16) {
+    // bf16 dQ leaves as whole-line pieces with 16-byte stores: the 128 x 576 tile is staged in
+    // the (now free) stages in two column parts, columns 0-319 (the waves' column blocks v < 5)
+    // and 320-575 (v >= 5), every wave staging its own blocks of both row halves at once; then
+    // every thread stores its share of the part's 16-byte pieces.  Stored straight from the
+    // accumulators (one 2-byte value per lane and instruction, 144 store instructions per lane)
+    // the kernel took 168 us at the config-5 shapes, staged 161 us.  The row pitch (part width
+    // + 16 bytes) puts the four row groups of a staging write on distinct banks.
+#pragma unroll
+    for (int part = 0; part < 2; ++part) {
+      const int v0 = part == 0 ? 0 : 5, v1 = part == 0 ? 5 : 9;
+      const int c0 = 16 * 4 * v0;                 // first column of the part
+      const int width = 16 * 4 * (v1 - v0);       // 320 or 256 columns
+      const int pitch = 2 * width + 16;
+      __syncthreads();   // the stages (first part) or the previous part's pieces are read out
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int v = v0; v < v1; ++v)
+            *reinterpret_cast<DMLA_LDS bf16*>(lds + (64 * rh + 16 * rq + 4 * g + i) * pitch +
+                                             (16 * (wc + 4 * v) - c0 + l16) * 2) = (bf16)(acc[rq][v][i] * unscale);
+      __syncthreads();
+      const int per_row = width / 8;              // 40 or 32 pieces
+#pragma unroll
+      for (int it = 0; it < 10; ++it) {
+        const int j = it * kDqThreads + (int)threadIdx.x;
+        if (j >= kDqRows * per_row) break;
+        const int rl = j / per_row, c = j - rl * per_row;
+        const int r = row0 + rl;
+        if (r >= p.R) continue;
+        const bf16x8 piece = *reinterpret_cast<const DMLA_LDS bf16x8*>(lds + rl * pitch + 16 * c);
+        const int pos = fast_div(r, p.hdiv), h = r - pos * p.H;
+        *reinterpret_cast<bf16x8*>(static_cast<bf16*>(p.dq) + b * p.dq_sb + h * p.dq_sh + pos * p.dq_ss + c0 + 8 * c) = piece;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int rq = 0; rq < 4; ++rq) {
 #pragma unroll
@@ -938,6 +978,7 @@ extern "C" int dmla_bwd_cache_latent(const void* q, const void* k_lat, const voi
   p.dq = dq;
   p.dk = dk_lat;
   p.dq_fp32 = dq_fp32 ? 1 : 0;
+  p.dq_rows16 = !dq_fp32 && mult8(dq_sb) && mult8(dq_sh) && mult8(dq_ss);
   p.dk_fp32 = dk_fp32 ? 1 : 0;
   p.q_sb = q_sb; p.q_sh = q_sh; p.q_ss = q_ss;
   p.k_sb = k_sb; p.k_ss = k_ss;

@@ -132,6 +132,37 @@ def test_bwd_strided_views_and_fp32_outputs(gpu):
 
 
 @pytest.mark.gpu
+def test_bwd_dq_row_stride_not_a_multiple_of_8(gpu):
+    # A bf16 dq whose strides are multiples of 8 elements leaves as whole 16-byte pieces staged
+    # through LDS; any other stride takes the per-element stores.  Both store the same rounded
+    # accumulators, so a dq written into a [.., 577]-wide buffer equals the contiguous one bit
+    # for bit (and the 577th column stays untouched).
+    from python import _lib
+    B, H, Sq, Sk = 1, 16, 200, 200
+    q, k, do = (t.to(gpu) for t in _inputs(B, H, Sq, Sk, seed=77))
+    o, m, l = ops.flash_dmla_fwd(q, k, 512, SCALE, True)
+    dq_ref, dk_ref = ops.flash_dmla_bwd(q, k, o, do, m, l, 512, SCALE, True)
+    wide = torch.full((B, H, Sq, 577), 7.0, dtype=torch.bfloat16, device=gpu)
+    dq = wide[..., :576]
+    dk = torch.empty_like(dk_ref)
+    ws_bytes = int(_lib.lib().dmla_bwd_workspace_bytes(B, H, Sq, Sk, 576, 512, 1))
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=gpu)
+    _lib.call(
+        "dmla_bwd_cache_latent",
+        ops._ptr(q), ops._ptr(k), ops._ptr(o), ops._ptr(do), ops._ptr(m), ops._ptr(l), ops._ptr(dq), ops._ptr(dk),
+        B, H, Sq, Sk, 576, 512,
+        q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1),
+        o.stride(0), o.stride(1), o.stride(2), do.stride(0), do.stride(1), do.stride(2),
+        dq.stride(0), dq.stride(1), dq.stride(2), dk.stride(0), dk.stride(1),
+        0, 1, SCALE, 1, ops._ptr(ws), ws_bytes, ops._stream(q),
+    )
+    torch.cuda.synchronize()
+    assert torch.equal(dq, dq_ref), "strided bf16 dq differs from the contiguous one"
+    assert torch.equal(dk, dk_ref)
+    assert (wide[..., 576] == 7.0).all(), "the column past dq was written"
+
+
+@pytest.mark.gpu
 def test_bwd_config5_full_shape(gpu):
     # benchmark config 5: B=4, H=16, S=2048, causal, dO ~ N(0, 1); references in fp32 on the GPU.
     q, k, do = _inputs(4, 16, 2048, 2048, seed=0)
