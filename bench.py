@@ -557,6 +557,69 @@ def trace_summary(trace_dir):
     return out
 
 
+def shape_sweep(steps, warmup):
+    """One JSON line per (workload, shape): the prefill, the paged decode and the cache-latent
+    backward around their benchmark configurations, with the same timing (GPU time of the
+    timed steps per step) and work accounting as the main lines.  Not part of the driver's
+    contract; it shows how the kernels behave away from the one benchmarked shape."""
+    import torch
+
+    from python import ops
+
+    dev = torch.device("cuda:0")
+    out = []
+    for B, S in ((16, 512), (8, 1024), (4, 2048), (2, 4096), (1, 8192)):
+        H = 16
+        q = _seeded((B, H, S, 576), 0, 0.5, torch.bfloat16).to(dev)
+        k = _seeded((B, S, 576), 1, 0.5, torch.bfloat16).to(dev)
+        flops = B * H * S * (S + 1) * (576 + 512)
+        _, ks = _time_launches(lambda i=0: ops.flash_dmla_fwd(q, k, 512, SCALE, True), steps, warmup)
+        rate = flops / (ks["region_ms"] * 1e-3) / 1e12
+        out.append({"workload": "prefill", "B": B, "H": H, "S": S, "ms": ks["region_ms"], "TFLOP/s": rate,
+                    "frac": rate / PEAK_BF16_TFLOPS})
+        del q, k
+    P, H = 64, 128
+    for B in (16, 64, 256):
+        g = torch.Generator().manual_seed(3)
+        lens = torch.randint(1024, 8193, (B,), generator=g)
+        n_pages = (lens + P - 1) // P
+        total, max_pages = int(n_pages.sum()), int(n_pages.max())
+        pools, tables = [], []
+        for r in range(3):
+            gr = torch.Generator().manual_seed(100 + r)
+            pools.append((torch.randn(total, P, 576, generator=gr) * 0.5).to(torch.bfloat16).to(dev))
+            perm = torch.randperm(total, generator=gr)
+            table = torch.zeros(B, max_pages, dtype=torch.int32)
+            c = 0
+            for bb in range(B):
+                n = int(n_pages[bb])
+                table[bb, :n] = perm[c:c + n].to(torch.int32)
+                c += n
+            tables.append(table.to(dev))
+        q = _seeded((B, H, 576), 4, 0.5, torch.bfloat16).to(dev)
+        sl = lens.to(torch.int32).to(dev)
+        nbytes = int(lens.sum()) * 576 * 2 + q.numel() * 2 + B * H * 512 * 2 + tables[0].numel() * 4 + B * 4
+        _, ks = _time_launches(
+            lambda i=0: ops.flash_dmla_decode_paged(q, pools[i % 3], tables[i % 3], sl, 512, SCALE), steps, warmup)
+        rate = nbytes / (ks["region_ms"] * 1e-3) / 1e9
+        out.append({"workload": "decode", "B": B, "H": H, "ctx": "1024..8192", "ms": ks["region_ms"], "GB/s": rate,
+                    "frac": rate / PEAK_HBM_GBS})
+        del pools, tables, q
+    for B, S in ((8, 1024), (4, 2048), (2, 4096), (1, 8192)):
+        H = 16
+        q = _seeded((B, H, S, 576), 0, 0.5, torch.bfloat16).to(dev)
+        k = _seeded((B, S, 576), 1, 0.5, torch.bfloat16).to(dev)
+        do = _seeded((B, H, S, 512), 2, 1.0, torch.bfloat16).to(dev)
+        o, m, l = ops.flash_dmla_fwd(q, k, 512, SCALE, True)
+        flops = B * H * S * (S + 1) * (3 * 576 + 2 * 512)
+        _, ks = _time_launches(lambda i=0: ops.flash_dmla_bwd(q, k, o, do, m, l, 512, SCALE, True), steps, warmup)
+        rate = flops / (ks["region_ms"] * 1e-3) / 1e12
+        out.append({"workload": "bwd", "B": B, "H": H, "S": S, "ms": ks["region_ms"], "TFLOP/s": rate,
+                    "frac": rate / PEAK_BF16_TFLOPS})
+        del q, k, do, o, m, l
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -568,6 +631,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget per workload")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run MIB-sized device copies (HBM counter calibration) and exit")
+    ap.add_argument("--sweep", action="store_true",
+                    help="only time prefill, decode and backward over a range of shapes (one JSON line each) and exit")
     ap.add_argument("--trace-summary", metavar="DIR", default=None,
                     help="summarise a rocprofv3 --kernel-trace --marker-trace CSV output directory of a bench run "
                          "(the kernels inside each workload's timed range) and exit; needs no GPU")
@@ -588,6 +653,10 @@ def main():
         sys.exit(1)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.sweep:
+        for rec in shape_sweep(args.steps, args.warmup):
+            print(json.dumps(rec), flush=True)
         return
     cpu = 0.0 if args.no_cpu_baseline else args.cpu_seconds
     primary = bench_prefill(args.steps, args.warmup, cpu)
