@@ -227,7 +227,7 @@ def test_autograd_function_matches_fp32_autograd(gpu):
     ],
 )
 def test_bwd_row_chunks(gpu, monkeypatch, B, H, Sq, Sk, causal, dk_dtype):
-    # A 96 KB cap on dS' storage (the default is 512 MiB) cuts these rows into several chunks of
+    # A 96 KB cap on dS' storage (the default is 2 GiB) cuts these rows into several chunks of
     # 128-row groups; each chunk's dq rows are final and dk_lat sums over the chunks.
     monkeypatch.setenv("DMLA_BWD_DS_CAP_BYTES", str(96 * 1024))
     from python import _lib
@@ -253,10 +253,12 @@ def test_bwd_row_chunks(gpu, monkeypatch, B, H, Sq, Sk, causal, dk_dtype):
 
 
 @pytest.mark.gpu
-def test_bwd_long_sequence_is_chunked(gpu):
-    # S = 8192 (B = 1, H = 16): the causal dS' blocks alone are ~1.1 GB, more than the 512 MiB
-    # cap, so the rows run in three chunks; references in fp32 on the GPU.
+def test_bwd_long_sequence_is_chunked(gpu, monkeypatch):
+    # S = 8192 (B = 1, H = 16): the causal dS' blocks alone are ~1.1 GB; under a 512 MiB cap
+    # (the default 2 GiB holds them in one chunk) the rows run in three chunks; references in
+    # fp32 on the GPU.
     from python import _lib
+    monkeypatch.setenv("DMLA_BWD_DS_CAP_BYTES", str(512 << 20))
     ws = _lib.lib().dmla_bwd_workspace_bytes(1, 16, 8192, 8192, 576, 512, 1)
     assert ws < (512 << 20) + (200 << 20), ws
     q, k, do = _inputs(1, 16, 8192, 8192, seed=5)
