@@ -48,33 +48,33 @@ def _cases(kind, n, seed):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,H,Sq,Sk,causal", _cases("fwd", 6, 101))
+@pytest.mark.parametrize("B,H,Sq,Sk,causal", _cases("fwd", 12, 101))
 def test_random_fwd(gpu, B, H, Sq, Sk, causal):
     q, k = F._inputs(B, H, Sq, Sk, seed=B * 7919 + H * 31 + Sq)
     F._check(gpu, q, k, causal)
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,H,Sq,Sk,causal", _cases("bwd", 6, 102))
+@pytest.mark.parametrize("B,H,Sq,Sk,causal", _cases("bwd", 12, 102))
 def test_random_bwd(gpu, B, H, Sq, Sk, causal):
     q, k, do = BW._inputs(B, H, Sq, Sk, seed=B * 7919 + H * 31 + Sq)
     BW._check(gpu, q, k, do, causal, autograd=False)
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("lens,H,extra_pages", _cases("decode", 6, 103))
+@pytest.mark.parametrize("lens,H,extra_pages", _cases("decode", 12, 103))
 def test_random_decode(gpu, lens, H, extra_pages):
     q, pool, table, lt = D._paged(list(lens), H, seed=len(lens) * 131 + H, extra_pages=extra_pages)
     D._check(gpu, q, pool, table, lt)
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,H,Sq,Sk,causal", _cases("otf", 5, 104))
+@pytest.mark.parametrize("B,H,Sq,Sk,causal", _cases("otf", 10, 104))
 def test_random_onthefly_fwd(gpu, B, H, Sq, Sk, causal):
     OF._check(gpu, B, H, Sq, Sk, causal, seed=B * 7919 + H * 31 + Sq)
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,H,Sq,Sk,causal", _cases("otf_bwd", 5, 105))
+@pytest.mark.parametrize("B,H,Sq,Sk,causal", _cases("otf_bwd", 10, 105))
 def test_random_onthefly_bwd(gpu, B, H, Sq, Sk, causal):
     OB._check(gpu, B, H, Sq, Sk, causal, seed=B * 7919 + H * 31 + Sq, autograd=False)
