@@ -64,6 +64,30 @@ def test_decode_small(gpu, lens, H):
 
 
 @pytest.mark.gpu
+def test_decode_score_growth_takes_the_exact_max_pass(gpu):
+    # Each sequence's scores grow along its context by ~86 (log2 units) -- far past the 2^32
+    # headroom over a segment's first-tile max -- so every segment restarts on the exact-max
+    # path; the long contexts also split across workgroups, whose partials the combine merges.
+    lens = [700, 2100, 37, 64]
+    H, page = 128, 64
+    q, pool, table, sl = _paged(lens, H, seed=17)
+    pool = pool.float()
+    q = q.float()
+    for b, n in enumerate(lens):
+        for t in range(n):
+            pool[int(table[b, t // page]), t % page, 512] = 30.0 * t / max(n - 1, 1)
+    q[..., 512] = 4.0
+    q, pool = q.to(torch.bfloat16), pool.to(torch.bfloat16)
+    o, lse = ops.flash_dmla_decode_paged(q.to(gpu), pool.to(gpu), table.to(gpu), sl.to(gpu), 512, 0.5,
+                                         return_lse=True)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = R.dmla_decode_paged(q.float(), pool.float(), table, sl, 512, 0.5)
+    assert_out_close(o, o_ref)
+    d = (lse.cpu() - lse_ref).abs().max().item()
+    assert d <= 1e-3, f"lse max-abs {d:.3e}"
+
+
+@pytest.mark.gpu
 def test_decode_page_order_does_not_matter(gpu):
     q, pool, table, sl = _paged([500, 333], 128, seed=11)
     o1 = ops.flash_dmla_decode_paged(q.to(gpu), pool.to(gpu), table.to(gpu), sl.to(gpu), 512, SCALE)
