@@ -457,34 +457,55 @@ __global__ void __launch_bounds__(256, 2) otf_bwd_dkdv_kernel(OtfBwdParams p) {
     if (s + 1 < n_st) stage_iter(s + 1, std::integral_constant<int, 1>{}, Clean{});
   }
   // dK_lat = scale dS^T Q and dV_lat = P^T dO as bf16 hi / lo planes (keys past Sk hold zeros:
-  // P = 0 there)
+  // P = 0 there).  A lane holds dims 16 db + 4 g .. + 3 of key 16 kb + l16; one lane-row swap
+  // (rows of 16 lanes) per dword between the pieces of db = 2 dp and 2 dp + 1 leaves lane g with
+  // dims 32 dp + 16 (g & 1) + 8 (g >> 1) .. + 7, so each store is 16 bytes a lane and 64
+  // contiguous bytes a key row.
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
   const size_t plane = (size_t)BH * p.Skp * kLat;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
-    bf16* row = p.dxlat + ((size_t)bh * p.Skp + k0 + 16 * kb + l16) * kLat + 4 * g;
+    bf16* row = p.dxlat + ((size_t)bh * p.Skp + k0 + 16 * kb + l16) * kLat + 16 * (g & 1) + 8 * (g >> 1);
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      float a[4], c[4];
-      __bf16 ah[4], al[4], ch[4], cl[4];
+    for (int dp = 0; dp < 2; ++dp) {
+      u32x2 pc[4][2];   // [plane][db - 2 dp]
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[i] = dkt[db][kb][i] * p.scale;
-        c[i] = dvt[db][kb][i];
+      for (int j = 0; j < 2; ++j) {
+        const int db = 2 * dp + j;
+        float a[4], c[4];
+        __bf16 ah[4], al[4], ch[4], cl[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          a[i] = dkt[db][kb][i] * p.scale;
+          c[i] = dvt[db][kb][i];
+        }
+        split_bf16_rn(a, ah, al);
+        split_bf16_rn(c, ch, cl);
+        bf16x4 vah, val, vch, vcl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          vah[i] = ah[i];
+          val[i] = al[i];
+          vch[i] = ch[i];
+          vcl[i] = cl[i];
+        }
+        pc[0][j] = __builtin_bit_cast(u32x2, vah);
+        pc[1][j] = __builtin_bit_cast(u32x2, val);
+        pc[2][j] = __builtin_bit_cast(u32x2, vch);
+        pc[3][j] = __builtin_bit_cast(u32x2, vcl);
       }
-      split_bf16_rn(a, ah, al);
-      split_bf16_rn(c, ch, cl);
-      bf16x4 vah, val, vch, vcl;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        vah[i] = ah[i];
-        val[i] = al[i];
-        vch[i] = ch[i];
-        vcl[i] = cl[i];
+      for (int q = 0; q < 4; ++q) {
+        u32x4 v;
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+          const auto r = __builtin_amdgcn_permlane16_swap(pc[q][0][w], pc[q][1][w], false, false);
+          v[w] = r[0];
+          v[2 + w] = r[1];
+        }
+        *reinterpret_cast<u32x4*>(row + q * plane + 32 * dp) = v;
       }
-      *reinterpret_cast<bf16x4*>(row + 16 * db) = vah;
-      *reinterpret_cast<bf16x4*>(row + plane + 16 * db) = val;
-      *reinterpret_cast<bf16x4*>(row + 2 * plane + 16 * db) = vch;
-      *reinterpret_cast<bf16x4*>(row + 3 * plane + 16 * db) = vcl;
     }
   }
 }
