@@ -413,7 +413,7 @@ def bench_bwd(steps, warmup, cpu_baseline):
         "config": {"workload": "cache-latent backward (benchmark config 5)", "batch": B, "heads": H, "seq_len": S,
                    "d_qk": 576, "d_v": 512, "causal": True, "softmax_scale": SCALE},
         "roofline": _roofline("mfma", flops, ks, PEAK_BF16_TFLOPS, "TFLOP/s", _load_traffic("bwd"),
-                              "bwd_prep + bwd_kt + bwd_dkdv + bwd_dq + bwd_dk_reduce", "algorithmic_flops_per_launch"),
+                              "bwd_prep + bwd_kt + bwd_dkdv + bwd_dq (dK_lat reduction in its trailing workgroups)", "algorithmic_flops_per_launch"),
     }
     if cpu_baseline:
         res["cpu_baseline"] = cpu_bwd(q.cpu(), k.cpu(), o.cpu(), do.cpu(), m.cpu(), l.cpu(), flops, cpu_baseline)

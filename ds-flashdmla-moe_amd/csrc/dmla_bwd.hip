@@ -9,14 +9,15 @@
 // with P = exp(scale q.k - m) / l rebuilt from the forward's statistics (README.md:12).
 //
 // Rows are (query position, head) pairs with the head fastest, as in the forward, so the 16
-// heads of a position share one causal key range.  Five kernels run in order on one stream:
+// heads of a position share one causal key range.  Four kernels run in order on one stream:
 //   bwd_prep_kernel       per row: lse2 = (m + ln l) log2(e) and D = rowsum(dO * O);
 //   bwd_kt_kernel         K_lat^T in fp16 (32-key tiles of dims x keys, zero padded): dQ's B operand;
 //   bwd_dkdv_kernel       per 64-key block, streaming 32-row tiles: S, P, dP and dS' = scale dS
 //                         on MFMA, dK_lat accumulated in registers (V fold included), dS'
 //                         written once to HBM as fp16 16x16 blocks;
-//   bwd_dq_kernel         dQ = dS' K_lat per 128-row tile over its causal key range;
-//   bwd_dk_reduce_kernel  sums the dK_lat partials of the row segments in a fixed order.
+//   bwd_dq_kernel         dQ = dS' K_lat per 128-row tile over its causal key range; its
+//                         trailing workgroups sum the dK_lat partials of the row segments in
+//                         a fixed order.
 // No atomics anywhere: the result is bitwise deterministic.
 //
 // dS' is stored only where it is written: for each 128-row group, the 64-key blocks that some
@@ -620,6 +621,8 @@ bwd_dkdv_kernel(BwdParams p) {
 // C-order blocks through ds_read_b64_tr_b16, K^T (B operand) with b128 reads.  Tiles flow
 // through a 3-slot ring: the copies of tile kt+2 go out between the MFMAs of tile kt, so the
 // dS' blocks (read from HBM) have two tiles of time to land.
+__device__ __forceinline__ void dk_reduce_unit(const BwdParams& p, int b, int kb, int kbl, int t);
+
 __global__ void __launch_bounds__(kDqThreads, 1) bwd_dq_kernel(BwdParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[kDqLds];
   DMLA_LDS char* lds = (DMLA_LDS char*)smem;
@@ -627,6 +630,14 @@ __global__ void __launch_bounds__(kDqThreads, 1) bwd_dq_kernel(BwdParams p) {
   const int lane = lane_id();
   // The chunk's 128-row tiles (its row groups), heaviest (latest) first.
   const int g_end = (p.rt_end + 3) / 4;
+  const int n_dq = p.B * (g_end - p.rt_begin / 4);
+  if ((int)blockIdx.x >= n_dq) {
+    // Past the dQ tiles: the dK_lat reduction, two (b, key block, column quarter) units per
+    // workgroup, one per 256 threads.  These workgroups start as the dQ tiles drain.
+    const int u = 2 * ((int)blockIdx.x - n_dq) + (int)(threadIdx.x >> 8);
+    if (u < 4 * p.n_kb * p.B) dk_reduce_unit(p, u / (4 * p.n_kb), (u / 4) % p.n_kb, u % 4, (int)(threadIdx.x & 255));
+    return;
+  }
   const int b = (int)blockIdx.x % p.B;
   const int t = g_end - 1 - (int)blockIdx.x / p.B;
   const int row0 = kDqRows * t;
@@ -780,22 +791,23 @@ __global__ void __launch_bounds__(kDqThreads, 1) bwd_dq_kernel(BwdParams p) {
 }
 
 // ---- 5. dK_lat = sum of the segment partials ------------------------------------------------
-// One workgroup per (batch, 64-key block, 16-key block); the segments of the block are added in
-// part order, so the result does not depend on scheduling.  Thread t owns the 9 (column block,
+// One unit per (batch, 64-key block, 16-key block), run by 256 threads of a workgroup past the
+// dQ tiles of bwd_dq_kernel (they start as those tiles drain; a launch of its own measured
+// 20 us, the shared launch ~5 us less in the traced sum).  The segments of the block are added
+// in part order, so the result does not depend on scheduling.  Thread t owns the 9 (column block,
 // lane) slots t + 256 r of the 16 keys and loads all 9 of a part together (a wave reads 1 KB per
 // slot), so each wave keeps 9 KB in flight instead of one dependent load per slot (33 -> 19 us
 // at config 5; two parts at a time measured no faster).
 constexpr int kReduceSlots = kCb * 64 / 256;
 static_assert(kReduceSlots * 256 == kCb * 64, "the reduction's slots cover the partial evenly");
 
-__global__ void __launch_bounds__(256) bwd_dk_reduce_kernel(BwdParams p) {
-  const int b = blockIdx.z, kb = blockIdx.y, kbl = blockIdx.x;
+__device__ __forceinline__ void dk_reduce_unit(const BwdParams& p, int b, int kb, int kbl, int t) {
   const int pi = min(kb, p.n_kb - 1 - kb);
   const int ph = kb == pi ? 0 : 1;
   const PairPlan pp = pair_plan(p.causal, p.Sq, p.Sk, p.H, p.rt_begin, p.rt_end, p.n_kb, pi);
   const int iv_lo = ph == 0 ? 0 : pp.steps_a;
   const int iv_hi = ph == 0 ? pp.steps_a : pp.total;
-  const int t = threadIdx.x, ln = t & 63;
+  const int ln = t & 63;
   f32x4 s[kReduceSlots];
 #pragma unroll
   for (int r = 0; r < kReduceSlots; ++r) s[r] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1023,8 +1035,9 @@ extern "C" int dmla_bwd_cache_latent(const void* q, const void* k_lat, const voi
     p.last_chunk = c.g1 >= pl.n_groups ? 1 : 0;
     const int64_t grid_kv = 8 * ((c.n_items + 7) / 8);
     hipLaunchKernelGGL(bwd_dkdv_kernel, dim3((unsigned)grid_kv), dim3(kBwdThreads), 0, s, p);
-    hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)(B * (c.g1 - c.g0))), dim3(kDqThreads), 0, s, p);
-    hipLaunchKernelGGL(bwd_dk_reduce_kernel, dim3(4, (unsigned)pl.n_kb, (unsigned)B), dim3(256), 0, s, p);
+    // dQ tiles, then the dK_lat reduction's units two per workgroup (bwd_dq_kernel)
+    const int64_t n_red = ((int64_t)4 * pl.n_kb * B + 1) / 2;
+    hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)(B * (c.g1 - c.g0) + n_red)), dim3(kDqThreads), 0, s, p);
     g0 = c.g1;
   }
   return check_launch("dmla_bwd_cache_latent");
