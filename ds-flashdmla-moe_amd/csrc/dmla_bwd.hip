@@ -1015,7 +1015,9 @@ extern "C" int dmla_bwd_cache_latent(const void* q, const void* k_lat, const voi
   p.ds = reinterpret_cast<_Float16*>(ws + pl.off_ds);
   p.part = reinterpret_cast<float*>(ws + pl.off_part);
   p.dk_acc = dk_fp32 ? static_cast<float*>(dk_lat) : reinterpret_cast<float*>(ws + pl.off_acc);
-  if (B * ((int64_t)pl.n_groups) > 0x7fffffff)
+  // The dQ launch holds a chunk's row groups plus the reduction's units, two per workgroup; a
+  // dispatch counts its work-items in 32 bits.
+  if ((B * (int64_t)pl.n_groups + 2 * (int64_t)pl.n_kb * B) * kDqThreads > 0xffffffffll)
     return fail(DMLA_ERR_UNSUPPORTED, "dmla_bwd_cache_latent: grid too large");
 
   hipStream_t s = (hipStream_t)stream;
@@ -1036,7 +1038,7 @@ extern "C" int dmla_bwd_cache_latent(const void* q, const void* k_lat, const voi
     const int64_t grid_kv = 8 * ((c.n_items + 7) / 8);
     hipLaunchKernelGGL(bwd_dkdv_kernel, dim3((unsigned)grid_kv), dim3(kBwdThreads), 0, s, p);
     // dQ tiles, then the dK_lat reduction's units two per workgroup (bwd_dq_kernel)
-    const int64_t n_red = ((int64_t)4 * pl.n_kb * B + 1) / 2;
+    const int64_t n_red = (int64_t)2 * pl.n_kb * B;
     hipLaunchKernelGGL(bwd_dq_kernel, dim3((unsigned)(B * (c.g1 - c.g0) + n_red)), dim3(kDqThreads), 0, s, p);
     g0 = c.g1;
   }
